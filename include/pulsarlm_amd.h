@@ -1,0 +1,170 @@
+/*
+ * pulsarlm_amd: MI355X (gfx950) quantized-linear hot path, C ABI.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t passed
+ * as void* (NULL = the null stream), enqueues its work on that stream without
+ * synchronizing, and returns a plm_status. On failure the message (prefixed
+ * with the operation name, e.g. "gemm_int4_marlin: ...") is available from
+ * plm_last_error() on the calling thread. Inputs are never modified.
+ *
+ * Weight layout ("plm tile layout", opaque to callers): the N x K weight is cut
+ * into 16-row x 128-column tiles, strip-major (all K tiles of rows 0..15, then
+ * rows 16..31, ...). An int4 tile is 1 KiB: 64 lanes x 16 bytes, lane
+ * (n % 16) + 16 * ((k % 32) / 8) holding, in its four 32-bit words t = (k % 128)
+ * / 32, the 8 consecutive K values k % 8 of its column as offset-binary nibbles
+ * (q + 8), even k in nibbles 0-3 and odd k in nibbles 4-7. An fp8 tile is 2 KiB:
+ * two such 1 KiB halves (t / 2), each lane holding 8 bytes per t. Padding rows
+ * and columns hold q = 0. Scales are stored in their source dtype as
+ * [N/16 strips][ceil(K_pad / group_size) groups][16 or 1], one per column, or
+ * one per strip when block_n is a multiple of 16.
+ *
+ * Workspace: GEMMs that split K across workgroups need per-tile arrival
+ * counters (the first 64 KiB of the workspace) and fp32 partial sums (after them).
+ * plm_gemm_workspace_bytes() gives the size; the
+ * counter region must be zero before the first call that uses a workspace, and
+ * every call leaves it zero again, so one zeroed workspace can be reused by
+ * calls that are ordered on one stream. Calls that may overlap need separate
+ * workspaces.
+ */
+#ifndef PULSARLM_AMD_H
+#define PULSARLM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum plm_status {
+    PLM_OK = 0,
+    PLM_ERR_INVALID = 1,   /* bad argument: shape, dtype, size or alignment */
+    PLM_ERR_HIP = 2,       /* a HIP runtime call or kernel launch failed */
+    PLM_ERR_WORKSPACE = 3  /* workspace missing or smaller than required */
+} plm_status;
+
+typedef enum plm_dtype {
+    PLM_BF16 = 0,
+    PLM_FP16 = 1,
+    PLM_FP32 = 2
+} plm_dtype;
+
+typedef enum plm_format {
+    PLM_INT4 = 0, /* signed int4, symmetric, group-wise scales */
+    PLM_FP8 = 1   /* OCP e4m3 (fn); codes 0x7f/0xff (NaN) unsupported */
+} plm_format;
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* plm_last_error(void);
+
+/* Library version string. */
+const char* plm_version(void);
+
+/* Bytes of the repacked weight for an N x K matrix in `format`
+ * (counterpart of marlin_words, pulsarlm-core/src/kernels/marlin.cu:391-393). */
+int64_t plm_weight_bytes(plm_format format, int64_t n, int64_t k);
+
+/* Bytes of the repacked scales; -1 if the arguments are invalid. */
+int64_t plm_scale_bytes(int64_t n, int64_t k, int64_t block_n, int64_t group_size, plm_dtype scale_dtype);
+
+/*
+ * Repack int4 weights for the GEMMs.
+ * Replaces repack_int4_marlin_cuda (pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:317-322,
+ * pulsarlm-core/src/kernels/marlin.cu:601-620).
+ *   weight_packed  int32 [N, K/8], 8 signed nibbles per int32 along K, least significant first
+ *   weight_scale   [ceil(N/block_n), K/group_size] in scale_dtype, row-major
+ *   weight_out     plm_weight_bytes(PLM_INT4, N, K) bytes, 16-byte aligned
+ *   scale_out      plm_scale_bytes(...) bytes
+ * group_size must be a positive multiple of 16 dividing K; block_n > 0.
+ */
+int plm_repack_int4(const int32_t* weight_packed, const void* weight_scale, plm_dtype scale_dtype,
+                    int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                    void* weight_out, void* scale_out, void* stream);
+
+/* Repack e4m3 weights [N, K] (bytes). Replaces repack_fp8_marlin_cuda (ops.hpp:324-325,
+ * marlin.cu:622-629). */
+int plm_repack_fp8(const uint8_t* weight, const void* weight_scale, plm_dtype scale_dtype,
+                   int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                   void* weight_out, void* scale_out, void* stream);
+
+/*
+ * Convert weights already in the reference's Marlin layout (the (weight_marlin,
+ * scale_marlin) pair that repack_*_marlin_cuda returns: int32 words and fp32
+ * [K/group_size, ceil(N/block_n)] scales, marlin.cu:395-445) into the plm
+ * layout, so a checkpoint repacked for the reference can be loaded as is.
+ * The scales come out as PLM_FP32.
+ */
+int plm_convert_marlin(plm_format format, const int32_t* weight_marlin, const float* scale_marlin,
+                       int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                       void* weight_out, void* scale_out, void* stream);
+
+/* Dense dequantized weight [N, K] in out_dtype (PLM_BF16 or PLM_FP16) from the
+ * plm layout: W = round(q * round(scale)), round = RNE to out_dtype, exactly
+ * what the reference's kernels feed their MMAs (marlin.cu:123-151,180-194). */
+int plm_dequant(plm_format format, const void* weight, const void* scale, plm_dtype scale_dtype,
+                int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                void* out, plm_dtype out_dtype, void* stream);
+
+/* Workspace bytes plm_gemm may use for an [M, K] x [N, K]^T call (0 if none). */
+int64_t plm_gemm_workspace_bytes(plm_format format, int64_t m, int64_t n, int64_t k);
+
+/*
+ * y [M, N] = x [M, K] @ dequant(W)^T, x and y in x_dtype (PLM_BF16 or PLM_FP16),
+ * fp32 accumulation. Replaces gemm_int4_marlin_cuda / gemm_fp8_marlin_cuda
+ * (ops.hpp:327-343, marlin.cu:538-597,631-651).
+ * M <= 16 runs the bandwidth-first decode kernel; larger M the MFMA kernel.
+ * M == 0 or N == 0 returns PLM_OK without touching y.
+ */
+int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype,
+             const void* weight, const void* scale, plm_dtype scale_dtype,
+             int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+             void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * W8A8: x is quantized per row (token) to e4m3 on the fly, scale = amax/448,
+ * and multiplied with the fp8 weights on the fp8 MFMA. No counterpart in the
+ * reference (its fp8 path is W8A16); x and y bf16 or fp16.
+ */
+int plm_gemm_w8a8(const void* x, plm_dtype x_dtype,
+                  const void* weight, const void* scale, plm_dtype scale_dtype,
+                  int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                  void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Grouped GEMM over experts: rows [offsets[e-1], offsets[e]) of x (offsets
+ * int32 [n_experts], inclusive ends, as at::cumsum produces in
+ * pulsarlm-core/src/engine/model/paged_forward.cpp:120-121) are multiplied by
+ * expert e's weight. weight holds n_experts repacked [N, K] matrices back to
+ * back (plm_weight_bytes each), scale likewise (plm_scale_bytes each).
+ * Replaces one at::_grouped_mm(rows, W^T, offsets) call of routed_experts
+ * (paged_forward.cpp:124-125) for int4 experts.
+ */
+int plm_grouped_gemm(plm_format format, const void* x, plm_dtype x_dtype,
+                     const void* weight, const void* scale, plm_dtype scale_dtype,
+                     const int32_t* offsets, int64_t n_experts, int64_t rows,
+                     int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                     void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes plm_moe needs. */
+int64_t plm_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t n_experts,
+                                int64_t hidden, int64_t intermediate);
+
+/*
+ * routed_experts (paged_forward.cpp:108-130) for int4 experts and SiLU:
+ *   out [T, H] = sum_j top_weights[t, j] * down_e(silu(g) * u), (g | u) = gate_up_e(h[t]),
+ * e = top_experts[t, j] (int32 [T, top_k]), top_weights fp32 [T, top_k].
+ * gate_up holds n_experts repacked [2I, H] weights, down n_experts [H, I].
+ * Sorting by expert, offsets, gather, both grouped GEMMs, the activation and the
+ * weighted scatter-back all run on the device with no host synchronization.
+ */
+int plm_moe(const void* h, plm_dtype dtype, const int32_t* top_experts, const float* top_weights,
+            int64_t tokens, int64_t top_k, int64_t n_experts, int64_t hidden, int64_t intermediate,
+            const void* gate_up_weight, const void* gate_up_scale,
+            const void* down_weight, const void* down_scale, plm_dtype scale_dtype, int64_t group_size,
+            void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PULSARLM_AMD_H */

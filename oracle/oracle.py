@@ -1,0 +1,517 @@
+"""CPU oracle for the quantized-linear hot path.
+
+TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker (or, in the bench, as the timed CPU baseline). The product path
+(``pulsarlm_amd``) never imports it and has no CPU fallback.
+
+It restates, in numpy, the arithmetic of the reference's Marlin dequant-GEMM
+path in pulsarlm-core:
+
+* int4 packing, 8 signed nibbles per int32 along K, least significant first
+  (``pulsarlm-core/tests/kernels/test_marlin.cpp:42-46``,
+  ``pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:317-322``);
+* dequantization ``W = round(q * round(scale))`` in the activation dtype, i.e.
+  ``weight.to(dtype) * expanded_scale.to(dtype)`` (``test_marlin.cpp:48-50``),
+  which is what the kernel's ``scale_pair`` + ``__hmul2`` compute
+  (``pulsarlm-core/src/kernels/marlin.cu:78-84,123-151,180-194``);
+* e4m3 decode (``marlin.cu:176-194``) and the fp8 128x128 block quantizer of
+  ``pulsarlm-core/tests/model/test_qwen3_5.cpp:301-311``;
+* the Marlin word layout produced by ``repack_weight_kernel``
+  (``marlin.cu:86-117,154-171,197-236,391-393``);
+* dequantize-then-matmul with fp32 (here float64) accumulation
+  (``test_marlin.cpp:90-93,108-111``), output cast once to the activation dtype;
+* the non-repacked int4 GEMM's dequant ``round(q * fp32 scale)``
+  (``pulsarlm-core/src/kernels/int4_gemm.cu:136-138``);
+* the MoE ``routed_experts`` algorithm (``pulsarlm-core/src/engine/model/
+  paged_forward.cpp:108-130``) and the per-expert dense restatement of
+  ``pulsarlm-core/tests/model/test_qwen3_5_moe.cpp:229-248``.
+
+How each function is pinned (checks live in ``tests/test_oracle.py``):
+
+* ``bf16_round`` / ``fp16_round``: against torch's bf16/fp16 conversion on a
+  sweep including ties, subnormals and infinities.
+* ``e4m3_decode`` / ``e4m3_encode``: all 256 codes against torch's
+  ``float8_e4m3fn`` conversion; encode against torch on a dense sweep.
+* ``pack_int4`` / ``unpack_int4``: hand-computed known answers.
+* ``dequant``: every nibble x a scale sweep against the reference test's own
+  expression evaluated by ATen on the CPU (``q.to(dtype) * s.to(dtype)``).
+* ``marlin_encode_*``: known answers derived by hand from the lane/offset
+  description at ``marlin.cu:21-30,86-88,154-155``, and decode(encode(W)) == W.
+* ``gemm_ref``: against torch fp32 matmul, and the identity-GEMM closed form.
+* ``routed_experts_ref``: against the per-expert dense restatement.
+* ``fp8_block_quantize``: invariants (one code per block at |448|, exact
+  reconstruction bound) and against torch's e4m3 cast.
+* ``quantize_per_token_e4m3`` (W8A8 mode): parity unpinned by the reference,
+  which has no fp8-activation path; checked only against torch's e4m3 cast.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# Scalar formats
+# ---------------------------------------------------------------------------
+
+
+def bf16_round(x) -> np.ndarray:
+    """Round float32 values to bf16 with round-to-nearest-even; float32 result."""
+    f = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    bits = f.view(np.uint32).astype(np.uint64)
+    nan = np.isnan(f)
+    rounded = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16) << 16
+    out = (rounded & 0xFFFFFFFF).astype(np.uint32).view(np.float32).copy()
+    out[nan] = np.float32(np.nan)
+    return out
+
+
+def bf16_bits(x) -> np.ndarray:
+    return (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_from_bits(bits) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint32) << 16).astype(np.uint32).view(np.float32)
+
+
+def fp16_round(x) -> np.ndarray:
+    """Round float32 values to fp16 (numpy's cast is round-to-nearest-even)."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def round_to(x, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return bf16_round(x)
+    if dtype == "fp16":
+        return fp16_round(x)
+    raise ValueError(dtype)
+
+
+def e4m3_decode(codes) -> np.ndarray:
+    """OCP e4m3 (fn) byte -> float32. 0x7f/0xff are NaN; no infinities.
+
+    Normal: (1 + m/8) * 2^(e-7); subnormal (e == 0): m * 2^-9.
+    """
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = c & 7
+    mag = np.where(e == 0, m * 2.0**-9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    out = (sign * mag).astype(np.float32)
+    out[(c & 0x7F) == 0x7F] = np.nan
+    return out
+
+
+_E4M3_POS = e4m3_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)  # codes 0..126
+
+
+def e4m3_encode(x) -> np.ndarray:
+    """float32 -> e4m3 byte, round-to-nearest-even, non-saturating.
+
+    Magnitudes past the midpoint between 448 (0x7e) and the next grid value 480
+    become the NaN code, as torch's ``float8_e4m3fn`` cast does.
+    """
+    v = np.asarray(x, dtype=np.float32).astype(np.float64)
+    sign = np.signbit(v)
+    a = np.abs(v)
+    grid = np.concatenate([_E4M3_POS, [480.0]])  # index 127 stands for "overflow"
+    hi = np.searchsorted(grid, a, side="left")
+    hi = np.clip(hi, 0, 127)
+    lo = np.clip(hi - 1, 0, 127)
+    d_lo = np.abs(a - grid[lo])
+    d_hi = np.abs(grid[hi] - a)
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo)
+    code = np.where(a == grid[hi], hi, code)
+    code = np.where(np.isnan(v), 0x7F, code).astype(np.uint8)
+    code = np.where(code >= 0x7F, 0x7F, code).astype(np.uint8)
+    return (code | np.where(sign, 0x80, 0).astype(np.uint8)).astype(np.uint8)
+
+
+# ---------------------------------------------------------------------------
+# int4 packing (test_marlin.cpp:42-46; ops.hpp:317-322)
+# ---------------------------------------------------------------------------
+
+
+def pack_int4(q) -> np.ndarray:
+    """int values in [-8, 7], shape [N, K] (K % 8 == 0) -> int32 [N, K/8]."""
+    q = np.asarray(q, dtype=np.int64)
+    n, k = q.shape
+    assert k % 8 == 0
+    nib = (q & 0xF).reshape(n, k // 8, 8).astype(np.uint64)
+    shifts = (np.arange(8, dtype=np.uint64) * 4)
+    words = (nib << shifts).sum(axis=-1).astype(np.uint64)
+    return (words & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
+
+
+def unpack_int4(packed) -> np.ndarray:
+    """int32 [N, K/8] -> int8 [N, K], sign-extended nibbles, least significant first."""
+    p = np.asarray(packed, dtype=np.int32).view(np.uint32).astype(np.int64)
+    n, kw = p.shape
+    nib = (p[:, :, None] >> (np.arange(8) * 4)) & 0xF
+    q = nib - ((nib >> 3) << 4)
+    return q.reshape(n, kw * 8).astype(np.int8)
+
+
+def expand_scale(scale, n: int, k: int, block_n: int, group_size: int) -> np.ndarray:
+    """[ceil(N/bn), K/g] -> [N, K] (test_marlin.cpp:27-29)."""
+    s = np.asarray(scale, dtype=np.float32)
+    return np.repeat(np.repeat(s, block_n, axis=0)[:n], group_size, axis=1)[:, :k]
+
+
+def dequant_int4(packed, scale, block_n: int, group_size: int, dtype: str = "bf16") -> np.ndarray:
+    """Reference Marlin dequant: round(q * round(float(scale))) in ``dtype``; float32 result."""
+    q = unpack_int4(packed).astype(np.float32)
+    n, k = q.shape
+    s = round_to(expand_scale(scale, n, k, block_n, group_size), dtype)
+    return round_to(q * s, dtype)
+
+
+def dequant_fp8(codes, scale, block_n: int, group_size: int, dtype: str = "bf16") -> np.ndarray:
+    """Reference fp8 Marlin dequant: round(e4m3(code) * round(scale)) in ``dtype``."""
+    w = e4m3_decode(codes)
+    n, k = w.shape
+    s = round_to(expand_scale(scale, n, k, block_n, group_size), dtype)
+    return round_to(w * s, dtype)
+
+
+def dequant_int4_plain(packed, scale, group_size: int, dtype: str = "bf16") -> np.ndarray:
+    """Non-repacked int4 GEMM's dequant: round(q * fp32 scale) (int4_gemm.cu:136-138)."""
+    q = unpack_int4(packed).astype(np.float32)
+    n, k = q.shape
+    s = expand_scale(scale, n, k, 1, group_size)
+    return round_to(q * s, dtype)
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+
+
+def gemm_ref(x, w_deq, dtype: str | None = "bf16") -> np.ndarray:
+    """y = x @ W^T accumulated in float64 (>= the reference's fp32), cast once to ``dtype``."""
+    y = np.asarray(x, dtype=np.float64) @ np.asarray(w_deq, dtype=np.float64).T
+    y = y.astype(np.float32)
+    return y if dtype is None else round_to(y, dtype)
+
+
+def check_close(y, ref, atol=2e-2, rtol=2e-2, rel_l2=5e-3):
+    """The GEMM tolerance used throughout: elementwise |y-ref| <= atol + rtol*|ref|
+    (the reference test's ``allclose(2e-2, 2e-2)``, test_marlin.cpp:95,113) and
+    ||y-ref||_2 / ||ref||_2 <= rel_l2. Returns (ok, stats)."""
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    err = np.abs(y - ref)
+    denom = np.linalg.norm(ref)
+    l2 = float(np.linalg.norm(y - ref) / denom) if denom > 0 else float(np.linalg.norm(y - ref))
+    elem_ok = bool(np.all(err <= atol + rtol * np.abs(ref))) if err.size else True
+    stats = {
+        "max_abs": float(err.max()) if err.size else 0.0,
+        "rel_l2": l2,
+        "max_ref": float(np.abs(ref).max()) if ref.size else 0.0,
+    }
+    return elem_ok and l2 <= rel_l2 and np.all(np.isfinite(y)), stats
+
+
+# ---------------------------------------------------------------------------
+# The reference's Marlin word layout (marlin.cu:21-30,86-117,154-171,197-236)
+# ---------------------------------------------------------------------------
+
+MARLIN_TILE_N = 64
+MARLIN_SPAN_K = 32
+
+
+def marlin_words(n: int, k: int, words_per_lane: int) -> int:
+    """marlin.cu:391-393."""
+    return -(-n // MARLIN_TILE_N) * MARLIN_TILE_N // 8 * (-(-k // MARLIN_SPAN_K)) * words_per_lane * 32
+
+
+def _marlin_index(n: int, k: int, wpl: int):
+    total = marlin_words(n, k, wpl)
+    idx = np.arange(total, dtype=np.int64)
+    lane = idx % 32
+    rest = idx // 32
+    word = rest % wpl
+    rest //= wpl
+    subtile = rest % 8
+    rest //= 8
+    k_tiles = -(-k // MARLIN_SPAN_K)
+    k_tile = rest % k_tiles
+    block = rest // k_tiles
+    row = (block * 8 + subtile) * 8 + lane // 4
+    return idx, lane, word, k_tile, row
+
+
+_INT4_OFFSETS = np.array([0, 8, 16, 24, 1, 9, 17, 25], dtype=np.int64)
+
+
+def marlin_encode_int4(packed) -> np.ndarray:
+    """[N, K/8] int32 -> the reference's Marlin int32 words (marlin.cu:96-117,197-225)."""
+    q = unpack_int4(packed).astype(np.int64)
+    n, k = q.shape
+    idx, lane, word, k_tile, row = _marlin_index(n, k, 1)
+    pair = lane % 4
+    cols = k_tile[:, None] * 32 + 2 * pair[:, None] + _INT4_OFFSETS[None, :]
+    valid = (row[:, None] < n) & (cols < k)
+    vals = np.where(valid, q[np.minimum(row, n - 1)[:, None], np.minimum(cols, k - 1)], 0)
+    nib = np.where(valid, (vals & 0xF) ^ 8, 8).astype(np.uint64)
+    words = (nib << (np.arange(8, dtype=np.uint64) * 4)).sum(axis=1)
+    return (words & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
+
+
+def marlin_decode_int4(words, n: int, k: int) -> np.ndarray:
+    """Inverse of marlin_encode_int4: Marlin words -> int8 q [N, K]."""
+    w = np.asarray(words, dtype=np.int32).view(np.uint32).astype(np.int64)
+    idx, lane, word, k_tile, row = _marlin_index(n, k, 1)
+    pair = lane % 4
+    cols = k_tile[:, None] * 32 + 2 * pair[:, None] + _INT4_OFFSETS[None, :]
+    nib = (w[:, None] >> (np.arange(8) * 4)) & 0xF
+    vals = nib - 8  # nibbles hold (q & 0xF) ^ 8 == q + 8
+    q = np.zeros((n, k), dtype=np.int8)
+    valid = (row[:, None] < n) & (cols < k)
+    rr = np.broadcast_to(row[:, None], cols.shape)
+    q[rr[valid], cols[valid]] = vals[valid]
+    return q
+
+
+_FP8_OFFSETS = np.array([0, 1, 8, 9], dtype=np.int64)
+
+
+def marlin_encode_fp8(codes) -> np.ndarray:
+    """[N, K] e4m3 bytes -> the reference's Marlin words (marlin.cu:154-171,197-225)."""
+    c = np.asarray(codes, dtype=np.uint8)
+    n, k = c.shape
+    idx, lane, word, k_tile, row = _marlin_index(n, k, 2)
+    pair = lane % 4
+    cols = k_tile[:, None] * 32 + 16 * word[:, None] + 2 * pair[:, None] + _FP8_OFFSETS[None, :]
+    valid = (row[:, None] < n) & (cols < k)
+    b = np.where(valid, c[np.minimum(row, n - 1)[:, None], np.minimum(cols, k - 1)], 0).astype(np.uint64)
+    words = (b << (np.arange(4, dtype=np.uint64) * 8)).sum(axis=1)
+    return (words & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
+
+
+def marlin_decode_fp8(words, n: int, k: int) -> np.ndarray:
+    w = np.asarray(words, dtype=np.int32).view(np.uint32).astype(np.int64)
+    idx, lane, word, k_tile, row = _marlin_index(n, k, 2)
+    pair = lane % 4
+    cols = k_tile[:, None] * 32 + 16 * word[:, None] + 2 * pair[:, None] + _FP8_OFFSETS[None, :]
+    b = (w[:, None] >> (np.arange(4) * 8)) & 0xFF
+    out = np.zeros((n, k), dtype=np.uint8)
+    valid = (row[:, None] < n) & (cols < k)
+    rr = np.broadcast_to(row[:, None], cols.shape)
+    out[rr[valid], cols[valid]] = b[valid]
+    return out
+
+
+def marlin_scale(scale) -> np.ndarray:
+    """transpose_scale_kernel (marlin.cu:227-236): [rows, groups] -> fp32 [groups, rows]."""
+    return np.ascontiguousarray(np.asarray(scale, dtype=np.float32).T)
+
+
+# ---------------------------------------------------------------------------
+# fp8 quantizers
+# ---------------------------------------------------------------------------
+
+
+def fp8_block_quantize(w, block_n: int = 128, block_k: int = 128):
+    """test_qwen3_5.cpp:301-311: scale = max(amax(block), 1e-12) / 448 per
+    [block_n x block_k] block; codes = e4m3(w / expanded scale)."""
+    w = np.asarray(w, dtype=np.float32)
+    n, k = w.shape
+    rows = -(-n // block_n)
+    padded = np.zeros((rows * block_n, k), dtype=np.float32)
+    padded[:n] = w
+    amax = np.abs(padded).reshape(rows, block_n, k // block_k, block_k).max(axis=(1, 3))
+    scale = (np.maximum(amax, np.float32(1e-12)) / np.float32(448.0)).astype(np.float32)
+    expanded = expand_scale(scale, n, k, block_n, block_k)
+    codes = e4m3_encode((w / expanded).astype(np.float32))
+    return codes, scale
+
+
+def quantize_per_token_e4m3(x):
+    """W8A8 activation quantizer (no reference counterpart; parity unpinned by the
+    reference): per row, scale = max(amax, 1e-12)/448, codes = e4m3(x/scale)."""
+    x = np.asarray(x, dtype=np.float32)
+    amax = np.abs(x).max(axis=1) if x.size else np.zeros((x.shape[0],), np.float32)
+    scale = (np.maximum(amax, np.float32(1e-12)) / np.float32(448.0)).astype(np.float32)
+    codes = e4m3_encode((x / scale[:, None]).astype(np.float32))
+    return codes, scale
+
+
+def gemm_w8a8_ref(codes_x, scale_x, codes_w, scale_w, block_n: int, group_size: int, dtype="bf16"):
+    """y = diag(sx) * e4m3(cx) @ (e4m3(cw) * s_w)^T, exact products, float64 sums."""
+    xq = e4m3_decode(codes_x).astype(np.float64) * np.asarray(scale_x, np.float64)[:, None]
+    n, k = np.asarray(codes_w).shape
+    wq = e4m3_decode(codes_w).astype(np.float64) * expand_scale(scale_w, n, k, block_n, group_size)
+    return gemm_ref(xq, wq, dtype)
+
+
+# ---------------------------------------------------------------------------
+# MoE (paged_forward.cpp:108-130; test_qwen3_5_moe.cpp:229-248)
+# ---------------------------------------------------------------------------
+
+
+def silu(v):
+    v = np.asarray(v, dtype=np.float64)
+    return v / (1.0 + np.exp(-v))
+
+
+def moe_sort(top_experts, n_experts: int):
+    """Stable sort of the flattened (token, k) assignments by expert, per-expert
+    counts and inclusive-end int32 offsets (paged_forward.cpp:116-122)."""
+    te = np.asarray(top_experts, dtype=np.int64)
+    top_k = te.shape[-1]
+    flat = te.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    tokens = order // top_k
+    counts = np.bincount(flat, minlength=n_experts).astype(np.int32)
+    offsets = np.cumsum(counts).astype(np.int32)
+    return order, tokens, counts, offsets
+
+
+def routed_experts_ref(h, top_experts, top_weights, gate_up, down, dtype="bf16"):
+    """Restatement of routed_experts with dense per-expert weights (already
+    dequantized): gate_up [E, 2I, H], down [E, H, I]. Each GEMM accumulates in
+    float64 and rounds its output to ``dtype``, as the grouped GEMM's bf16
+    output does; silu(g)*u is rounded to ``dtype`` before the down GEMM; the
+    scatter-back sums in float64 and rounds once."""
+    h = np.asarray(h, dtype=np.float32)
+    e_count = gate_up.shape[0]
+    inter = gate_up.shape[1] // 2
+    order, tokens, counts, offsets = moe_sort(top_experts, e_count)
+    wflat = np.asarray(top_weights, dtype=np.float32).reshape(-1)[order]
+    rows = h[tokens]
+    out = np.zeros(h.shape, dtype=np.float64)
+    start = 0
+    for e in range(e_count):
+        end = int(offsets[e])
+        if end > start:
+            r = rows[start:end]
+            gu = gemm_ref(r, gate_up[e], dtype)
+            act = round_to(silu(gu[:, :inter]) * gu[:, inter:], dtype)
+            d = gemm_ref(act, down[e], dtype).astype(np.float64)
+            np.add.at(out, tokens[start:end], d * round_to(wflat[start:end], dtype)[:, None])
+        start = end
+    return round_to(out.astype(np.float32), dtype)
+
+
+def sparse_moe_ref(h, top_experts, top_weights, gate_up, down, dtype="bf16"):
+    """Per-expert dense restatement (test_qwen3_5_moe.cpp:229-248): each expert
+    over the tokens that chose it, with the same rounding points as
+    routed_experts_ref. Used to pin routed_experts_ref's sort/offset logic."""
+    h = np.asarray(h, dtype=np.float32)
+    te = np.asarray(top_experts)
+    tw = np.asarray(top_weights, dtype=np.float32)
+    inter = gate_up.shape[1] // 2
+    out = np.zeros(h.shape, dtype=np.float64)
+    for e in range(gate_up.shape[0]):
+        chosen = te == e
+        toks = np.nonzero(chosen.any(-1))[0]
+        if toks.size == 0:
+            continue
+        weight = (tw * chosen).sum(-1)[toks]
+        gu = gemm_ref(h[toks], gate_up[e], dtype)
+        act = round_to(silu(gu[:, :inter]) * gu[:, inter:], dtype)
+        d = gemm_ref(act, down[e], dtype).astype(np.float64)
+        out[toks] += d * round_to(weight, dtype)[:, None]
+    return round_to(out.astype(np.float32), dtype)
+
+
+# ---------------------------------------------------------------------------
+# Seeded synthetic inputs
+# ---------------------------------------------------------------------------
+
+
+def make_w4a16(m: int, n: int, k: int, group_size: int = 128, seed: int = 0, block_n: int = 1):
+    """x bf16-representable N(0,1) [M,K]; q uniform [-8,7]; fp16 scales |N(0,0.02)|+1e-3."""
+    rng = np.random.default_rng(seed)
+    x = bf16_round(rng.standard_normal((m, k), dtype=np.float32))
+    q = rng.integers(-8, 8, size=(n, k), dtype=np.int64)
+    rows = -(-n // block_n)
+    scale = (np.abs(rng.standard_normal((rows, k // group_size)).astype(np.float32) * 0.02) + 1e-3)
+    scale = scale.astype(np.float16)
+    return x, pack_int4(q), scale
+
+
+def make_fp8(m: int, n: int, k: int, seed: int = 0, block: int = 128):
+    """Weights = block quantizer applied to bf16 N(0, 0.02)."""
+    rng = np.random.default_rng(seed)
+    x = bf16_round(rng.standard_normal((m, k), dtype=np.float32))
+    w = bf16_round(rng.standard_normal((n, k), dtype=np.float32) * 0.02)
+    codes, scale = fp8_block_quantize(w, block, block)
+    return x, codes, scale
+
+
+def zipf_routing(tokens: int, n_experts: int, top_k: int, alpha: float = 1.2, seed: int = 0):
+    """top_k distinct experts per token drawn from Zipf(alpha) over expert ids
+    (without replacement); weights = renormalised softmax of seeded logits."""
+    rng = np.random.default_rng(seed)
+    p = 1.0 / np.arange(1, n_experts + 1) ** alpha
+    p /= p.sum()
+    experts = np.empty((tokens, top_k), dtype=np.int64)
+    for t in range(tokens):
+        experts[t] = rng.choice(n_experts, size=top_k, replace=False, p=p)
+    logits = rng.standard_normal((tokens, top_k)).astype(np.float32)
+    w = np.exp(logits - logits.max(-1, keepdims=True))
+    w = (w / w.sum(-1, keepdims=True)).astype(np.float32)
+    return experts, w
+
+
+# ---------------------------------------------------------------------------
+# The plm tile layout (this build's format; restated from its specification in
+# include/pulsarlm_amd.h so the GPU repack can be compared bit for bit)
+# ---------------------------------------------------------------------------
+
+
+def _plm_coords(n: int, k: int):
+    """For every (row, col) of an N x K matrix: strip, k tile, step t, lane, i."""
+    rows = np.arange(n)[:, None]
+    cols = np.arange(k)[None, :]
+    strip = rows // 16
+    kt = cols // 128
+    t = (cols % 128) // 32
+    lane = rows % 16 + 16 * ((cols % 32) // 8)
+    i = cols % 8
+    return strip, kt, t, lane, i
+
+
+def plm_layout_int4(packed) -> np.ndarray:
+    """int32 [N, K/8] -> plm int4 layout as uint32 words (padding nibbles = 8, i.e. q = 0)."""
+    q = unpack_int4(packed).astype(np.int64)
+    n, k = q.shape
+    strips, ktiles = -(-n // 16), -(-k // 128)
+    words = np.zeros(strips * ktiles * 256, dtype=np.uint64)
+    # Start from all-padding words, then clear and set each real nibble.
+    nib_all = np.full((strips * ktiles * 256, 8), 8, dtype=np.uint64)
+    strip, kt, t, lane, i = _plm_coords(n, k)
+    widx = ((strip * ktiles + kt) * 64 + lane) * 4 + t
+    pos = np.broadcast_to(np.where(i % 2 == 1, 4 + i // 2, i // 2), widx.shape)
+    nib_all[widx.reshape(-1), pos.reshape(-1)] = ((q & 0xF) ^ 8).reshape(-1).astype(np.uint64)
+    words = (nib_all << (np.arange(8, dtype=np.uint64) * 4)).sum(axis=1)
+    return (words & 0xFFFFFFFF).astype(np.uint32)
+
+
+def plm_layout_fp8(codes) -> np.ndarray:
+    """uint8 [N, K] -> plm fp8 layout bytes (padding 0)."""
+    c = np.asarray(codes, dtype=np.uint8)
+    n, k = c.shape
+    strips, ktiles = -(-n // 16), -(-k // 128)
+    out = np.zeros(strips * ktiles * 2048, dtype=np.uint8)
+    strip, kt, t, lane, i = _plm_coords(n, k)
+    off = ((strip * ktiles + kt) * 2 + t // 2) * 1024 + lane * 16 + (t % 2) * 8 + i
+    out[np.broadcast_to(off, c.shape).reshape(-1)] = c.reshape(-1)
+    return out
+
+
+def plm_layout_scale(scale, n: int, k: int, block_n: int, group_size: int) -> np.ndarray:
+    """[ceil(N/bn), K/g] -> [strips, groups, cols] in the same dtype (padding 0)."""
+    s = np.asarray(scale)
+    strips, ktiles = -(-n // 16), -(-k // 128)
+    groups = -(-(ktiles * 128) // group_size)
+    cols = 1 if block_n % 16 == 0 else 16
+    out = np.zeros((strips, groups, cols), dtype=s.dtype)
+    for c in range(cols):
+        col = np.arange(strips) * 16 + c
+        ok = col < n
+        out[ok, : k // group_size, c] = s[col[ok] // block_n]
+    return out

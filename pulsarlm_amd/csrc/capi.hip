@@ -1,0 +1,90 @@
+// C-ABI GEMM entry points: argument checks (mirroring gemm<fmt>,
+// pulsarlm-core/src/kernels/marlin.cu:538-576) and dispatch between the decode
+// kernel (M <= 16, the reference's small_m switch at marlin.cu:577) and the MFMA
+// kernel.
+#include "plm_common.hpp"
+
+namespace plm {
+int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
+                  plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                  void* y, void* workspace, size_t workspace_bytes, hipStream_t s);
+int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
+                plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y,
+                void* workspace, size_t workspace_bytes, hipStream_t s);
+int64_t decode_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k);
+int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k);
+
+constexpr int64_t kDecodeMaxM = 16;
+
+const char* gemm_op_name(plm_format f) { return f == PLM_INT4 ? "gemm_int4_marlin" : "gemm_fp8_marlin"; }
+
+int check_gemm(const char* op, plm_format f, const void* x, plm_dtype x_dtype, const void* w, const void* scale,
+               plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+               const void* y) {
+    PLM_CHECK_ARG(f == PLM_INT4 || f == PLM_FP8, op, "unknown weight format");
+    PLM_CHECK_ARG(x_dtype == PLM_BF16 || x_dtype == PLM_FP16, op, "x must be fp16 or bf16");
+    PLM_CHECK_ARG(scale_dtype == PLM_BF16 || scale_dtype == PLM_FP16 || scale_dtype == PLM_FP32, op,
+                  "scale dtype must be bf16, fp16 or fp32");
+    PLM_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, op, "sizes must be non-negative");
+    PLM_CHECK_ARG(block_n > 0, op, "block_n must be positive");
+    PLM_CHECK_ARG(group_size > 0 && group_size % 16 == 0, op, "group_size must be a positive multiple of 16");
+    PLM_CHECK_ARG(k % group_size == 0, op, "K must be a multiple of group_size");
+    PLM_CHECK_ARG(n <= (int64_t{1} << 30) && k <= (int64_t{1} << 30) && m <= (int64_t{1} << 30), op,
+                  "sizes must be below 2^30");
+    if (m == 0 || n == 0) return PLM_OK;
+    PLM_CHECK_ARG(x != nullptr && w != nullptr && scale != nullptr && y != nullptr, op, "null pointer");
+    PLM_CHECK_ARG(aligned(x, 16), op, "x must be 16-byte aligned");
+    PLM_CHECK_ARG(aligned(w, 16), op, "weight must be 16-byte aligned");
+    PLM_CHECK_ARG(aligned(scale, 4), op, "scale must be 4-byte aligned");
+    PLM_CHECK_ARG(aligned(y, 2), op, "y must be 2-byte aligned");
+    return PLM_OK;
+}
+
+}  // namespace plm
+
+using namespace plm;
+
+extern "C" {
+
+int64_t plm_gemm_workspace_bytes(plm_format format, int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0) return 0;
+    return m <= kDecodeMaxM ? decode_workspace_bytes(format, m, n, k) : mfma_workspace_bytes(format, m, n, k);
+}
+
+int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype, const void* weight, const void* scale,
+             plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y,
+             void* workspace, size_t workspace_bytes, void* stream) {
+    const char* op = gemm_op_name(format);
+    clear_error();
+    if (int rc = check_gemm(op, format, x, x_dtype, weight, scale, scale_dtype, m, n, k, block_n, group_size, y))
+        return rc;
+    if (m == 0 || n == 0) return PLM_OK;
+    const bool bf16 = x_dtype == PLM_BF16;
+    if (m <= kDecodeMaxM)
+        return launch_decode(op, format, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y,
+                             workspace, workspace_bytes, as_stream(stream));
+    return launch_mfma(op, format, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, workspace,
+                       workspace_bytes, as_stream(stream));
+}
+
+}  // extern "C"
+
+// Entry points whose kernels are not built yet report so instead of running.
+extern "C" {
+int plm_gemm_w8a8(const void*, plm_dtype, const void*, const void*, plm_dtype, int64_t, int64_t, int64_t, int64_t,
+                  int64_t, void*, void*, size_t, void*) {
+    plm::set_error("gemm_fp8_w8a8", "not implemented");
+    return PLM_ERR_INVALID;
+}
+int plm_grouped_gemm(plm_format, const void*, plm_dtype, const void*, const void*, plm_dtype, const int32_t*, int64_t,
+                     int64_t, int64_t, int64_t, int64_t, int64_t, void*, void*, size_t, void*) {
+    plm::set_error("grouped_gemm", "not implemented");
+    return PLM_ERR_INVALID;
+}
+int64_t plm_moe_workspace_bytes(int64_t, int64_t, int64_t, int64_t, int64_t) { return 0; }
+int plm_moe(const void*, plm_dtype, const int32_t*, const float*, int64_t, int64_t, int64_t, int64_t, int64_t,
+            const void*, const void*, const void*, const void*, plm_dtype, int64_t, void*, void*, size_t, void*) {
+    plm::set_error("routed_experts", "not implemented");
+    return PLM_ERR_INVALID;
+}
+}

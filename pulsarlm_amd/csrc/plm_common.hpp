@@ -1,0 +1,274 @@
+// Shared definitions for the gfx950 quantized-linear kernels: the tile layout
+// constants, operand vector types, MFMA wrappers, dtype helpers and the C-ABI
+// error plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/pulsarlm_amd.h"
+
+namespace plm {
+
+// ---------------------------------------------------------------------------
+// Layout: 16 x 128 weight tiles, 64 lanes x 16 bytes per 1 KiB sub-tile.
+// ---------------------------------------------------------------------------
+constexpr int kTileN = 16;
+constexpr int kTileK = 128;
+constexpr int kSubTileBytes = 1024;
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+template <plm_format F> struct fmt_traits;
+template <> struct fmt_traits<PLM_INT4> {
+    static constexpr int tile_bytes = 1024;  // 16 x 128 x 4 bit
+};
+template <> struct fmt_traits<PLM_FP8> {
+    static constexpr int tile_bytes = 2048;  // 16 x 128 x 8 bit
+};
+
+inline int64_t tile_bytes(plm_format f) { return f == PLM_INT4 ? 1024 : 2048; }
+
+struct layout_dims {
+    int64_t strips;     // ceil(N / 16)
+    int64_t ktiles;     // ceil(K / 128)
+    int64_t groups;     // ceil(ktiles * 128 / group_size): scale groups incl. padding
+    int scale_cols;     // 16 (per column) or 1 (per strip)
+};
+
+inline layout_dims make_dims(int64_t n, int64_t k, int64_t block_n, int64_t group_size) {
+    layout_dims d;
+    d.strips = ceil_div(n, kTileN);
+    d.ktiles = ceil_div(k, kTileK);
+    d.groups = ceil_div(d.ktiles * kTileK, group_size);
+    d.scale_cols = (block_n % kTileN == 0) ? 1 : kTileN;
+    return d;
+}
+
+// Split-K workspaces start with a fixed region of arrival counters, so a
+// workspace reused across calls of different shapes always finds its counters
+// at the same place (and zero); partial sums follow it.
+constexpr int64_t kCounterBytes = 64 * 1024;
+constexpr int64_t kMaxCounters = kCounterBytes / 4;
+
+inline int dtype_size(plm_dtype t) { return t == PLM_FP32 ? 4 : 2; }
+
+// ---------------------------------------------------------------------------
+// Vector types for MFMA operands.
+// ---------------------------------------------------------------------------
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
+
+// 16x16x32 MFMA with fp32 accumulation; the operand is 8 16-bit values per lane
+// held as 4 packed dwords. A: lane l = row l%16, K block l/16. B: lane l = column
+// l%16, same K block. D: lane l = column l%16, rows 4*(l/16) + i.
+template <bool BF16>
+__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+    if constexpr (BF16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                      __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                     __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    }
+}
+
+// 16x16x128 fp8 x fp8 (both OCP e4m3) MFMA, 32 bytes per lane per operand.
+__device__ __forceinline__ f32x4_t mfma16x16x128_fp8(i32x8_t a, i32x8_t b, f32x4_t c) {
+    // cbsz = blgp = 0 selects e4m3 for both operands; scale exponents 127 = x1.
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit float helpers (bit level, RNE).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    // Round to nearest even; NaN stays NaN (quiet bit forced).
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+    return ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) & 0xffffu;
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+
+__device__ __forceinline__ float round_f16(float f) { return static_cast<float>(static_cast<_Float16>(f)); }
+
+template <bool BF16> __device__ __forceinline__ float round_to(float f) {
+    if constexpr (BF16) return round_bf16(f);
+    else return round_f16(f);
+}
+
+template <bool BF16> __device__ __forceinline__ uint32_t to_bits16(float f) {
+    if constexpr (BF16) return f32_to_bf16_bits(f);
+    else return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f)));
+}
+
+template <bool BF16> __device__ __forceinline__ float from_bits16(uint32_t b) {
+    if constexpr (BF16) return bf16_bits_to_f32(b);
+    else return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
+
+// Two fp32 -> one dword of two 16-bit values (lo = a), RNE.
+template <bool BF16> __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (BF16) {
+        typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+        bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+        return __builtin_bit_cast(uint32_t, v);
+    } else {
+        typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+        f16x2_t v = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+}
+
+// Scale load in its stored dtype -> fp32.
+__device__ __forceinline__ float load_scale(const void* base, int64_t index, int dtype) {
+    if (dtype == PLM_FP32) return static_cast<const float*>(base)[index];
+    const uint16_t b = static_cast<const uint16_t*>(base)[index];
+    if (dtype == PLM_BF16) return bf16_bits_to_f32(b);
+    return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+// e4m3 (fn) byte -> fp32, exact (subnormals included); the NaN codes are not handled.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+    const uint32_t sign = (c & 0x80u) << 24;
+    const uint32_t e = (c >> 3) & 0xfu, m = c & 7u;
+    // Normal: (1 + m/8) 2^(e-7) -> fp32 exponent e + 120. Subnormal: m 2^-9.
+    const uint32_t normal = ((e + 120u) << 23) | (m << 20);
+    const uint32_t sub = __float_as_uint(static_cast<float>(m) * 0.001953125f);
+    return __uint_as_float(sign | (e == 0 ? sub : normal));
+}
+
+// ---------------------------------------------------------------------------
+// Exact in-register dequantization to the MFMA operand: round(q * round(s)),
+// the value the reference's kernels feed their MMAs (pulsarlm-core/src/kernels/
+// marlin.cu:78-84,123-151,180-194).
+//
+// int4: a plm word holds K pair p = (2p, 2p+1) in nibbles p and p + 4 as u = q + 8.
+// One v_bitop3 turns two nibbles at bits 0-3 of each 16-bit half into the fp16
+// pair (1024 + u, 1024 + u'), or at bits 4-7 into (1024 + 16u, ...). v_fma_mix_f32
+// then computes (1024 + u) * s - 1032 s, resp. (1024 + 16u) * s/16 - 72 s, which
+// equals q * s with no rounding (every product and sum fits fp32's 24 bits), and
+// v_cvt_pk_{bf16,f16}_f32 rounds the pair once, to nearest even.
+// ---------------------------------------------------------------------------
+struct int4_scale {
+    float s0, c0;  // nibbles at bits 0-3:  s, -1032 s
+    float s1, c1;  // nibbles at bits 4-7:  s / 16, -72 s
+};
+
+template <bool BF16> __device__ __forceinline__ int4_scale make_int4_scale(float raw) {
+    const float s = round_to<BF16>(raw);
+    return {s, -1032.f * s, s * 0.0625f, -72.f * s};
+}
+
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+    return __builtin_amdgcn_bitop3_b32(a, mask, bits, 0xEA);  // (a & mask) | bits
+}
+
+__device__ __forceinline__ float half_lo(uint32_t h) {
+    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+    return static_cast<float>(__builtin_bit_cast(f16x2_t, h)[0]);
+}
+__device__ __forceinline__ float half_hi(uint32_t h) {
+    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+    return static_cast<float>(__builtin_bit_cast(f16x2_t, h)[1]);
+}
+
+template <bool BF16> __device__ __forceinline__ u32x4_t dq_int4(uint32_t w, const int4_scale& k) {
+    const uint32_t h0 = and_or(w, 0x000F000Fu, 0x64006400u);  // K0, K1
+    const uint32_t h1 = and_or(w, 0x00F000F0u, 0x64006400u);  // K2, K3 (x16)
+    const uint32_t w8 = w >> 8;
+    const uint32_t h2 = and_or(w8, 0x000F000Fu, 0x64006400u);  // K4, K5
+    const uint32_t h3 = and_or(w8, 0x00F000F0u, 0x64006400u);  // K6, K7 (x16)
+    u32x4_t b;
+    b[0] = pack2<BF16>(__builtin_fmaf(half_lo(h0), k.s0, k.c0), __builtin_fmaf(half_hi(h0), k.s0, k.c0));
+    b[1] = pack2<BF16>(__builtin_fmaf(half_lo(h1), k.s1, k.c1), __builtin_fmaf(half_hi(h1), k.s1, k.c1));
+    b[2] = pack2<BF16>(__builtin_fmaf(half_lo(h2), k.s0, k.c0), __builtin_fmaf(half_hi(h2), k.s0, k.c0));
+    b[3] = pack2<BF16>(__builtin_fmaf(half_lo(h3), k.s1, k.c1), __builtin_fmaf(half_hi(h3), k.s1, k.c1));
+    return b;
+}
+
+// fp8: v_cvt_pk_f32_fp8 decodes two e4m3 bytes exactly; the product with the
+// rounded scale is exact in fp32 (4 x 11 significant bits) and rounded once.
+template <bool BF16> __device__ __forceinline__ u32x4_t dq_fp8(uint32_t lo, uint32_t hi, float s) {
+    typedef __attribute__((ext_vector_type(2))) float f2;
+    u32x4_t b;
+    const f2 a0 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+    const f2 a1 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+    const f2 a2 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+    const f2 a3 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+    b[0] = pack2<BF16>(a0[0] * s, a0[1] * s);
+    b[1] = pack2<BF16>(a1[0] * s, a1[1] * s);
+    b[2] = pack2<BF16>(a2[0] * s, a2[1] * s);
+    b[3] = pack2<BF16>(a3[0] * s, a3[1] * s);
+    return b;
+}
+
+// ---------------------------------------------------------------------------
+// Split-K handshake. Partial sums are written and read with agent-scope relaxed
+// atomics, which gfx950 issues as sc1 (coherent) stores/loads that bypass the
+// per-XCD L2, so no agent-scope fence (an L2 writeback + invalidate of the whole
+// cache) is needed: a workgroup waits for its own stores to complete, then one
+// lane counts the arrival.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_partial(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_partial(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Call with every thread of the workgroup after its store_partial()s. Returns true
+// in every thread of the last workgroup to arrive at `counter`, which is then reset.
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, uint32_t* lds_flag) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = atomicAdd(counter, 1u);
+        const bool last = prev == expected - 1;
+        if (last) atomicExch(counter, 0u);
+        *lds_flag = last ? 1u : 0u;
+    }
+    __syncthreads();
+    return *lds_flag != 0;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side error plumbing.
+// ---------------------------------------------------------------------------
+void set_error(const char* op, const char* fmt, ...);
+void clear_error();
+
+#define PLM_CHECK_ARG(cond, op, ...)                 \
+    do {                                             \
+        if (!(cond)) {                               \
+            ::plm::set_error(op, __VA_ARGS__);       \
+            return PLM_ERR_INVALID;                  \
+        }                                            \
+    } while (0)
+
+#define PLM_HIP_LAUNCH_CHECK(op)                                                   \
+    do {                                                                           \
+        hipError_t e_ = hipGetLastError();                                         \
+        if (e_ != hipSuccess) {                                                    \
+            ::plm::set_error(op, "kernel launch failed: %s", hipGetErrorString(e_)); \
+            return PLM_ERR_HIP;                                                    \
+        }                                                                          \
+    } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int cu_count();
+
+}  // namespace plm

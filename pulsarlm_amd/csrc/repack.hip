@@ -1,0 +1,386 @@
+// Load-time conversions into the plm tile layout, the dense dequant, and the
+// C-ABI plumbing shared by every entry point (errors, sizes, device queries).
+//
+// Counterparts in the reference: repack_weight_kernel / transpose_scale_kernel /
+// repack<> (pulsarlm-core/src/kernels/marlin.cu:197-236,395-445) and its
+// exports repack_int4_marlin_cuda / repack_fp8_marlin_cuda (marlin.cu:601-629).
+#include <cstdarg>
+#include <mutex>
+#include <vector>
+
+#include "plm_common.hpp"
+
+namespace plm {
+
+namespace {
+thread_local std::string g_error;
+}
+
+void set_error(const char* op, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_error = std::string(op) + ": " + buf;
+}
+
+void clear_error() { g_error.clear(); }
+
+int cu_count() {
+    static std::mutex mu;
+    static std::vector<int> counts;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    if (static_cast<int>(counts.size()) <= dev) counts.resize(dev + 1, 0);
+    if (counts[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        counts[dev] = n;
+    }
+    return counts[dev];
+}
+
+namespace {
+
+// Source word (8 nibbles, LSB first, two's complement) -> plm word: offset
+// binary, even K in nibbles 0-3 and odd K in nibbles 4-7.
+__device__ __forceinline__ uint32_t plm_word_from_lsb_first(uint32_t src) {
+    uint32_t out = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t nib = ((src >> (4 * i)) & 0xfu) ^ 8u;
+        const int pos = (i & 1) ? 4 + (i >> 1) : (i >> 1);
+        out |= nib << (4 * pos);
+    }
+    return out;
+}
+
+// One thread per 32-bit word of the int4 layout: word ((strip*KT + kt)*64 + lane)*4 + t
+// holds column strip*16 + lane%16, K = kt*128 + 32t + 8*(lane/16) + 0..7.
+__global__ void repack_int4_kernel(const int32_t* __restrict__ src, uint32_t* __restrict__ dst, int64_t n,
+                                   int64_t k, int64_t ktiles, int64_t total) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int t = static_cast<int>(idx & 3);
+    const int lane = static_cast<int>((idx >> 2) & 63);
+    const int64_t tile = idx >> 8;
+    const int64_t kt = tile % ktiles;
+    const int64_t strip = tile / ktiles;
+    const int64_t col = strip * kTileN + (lane & 15);
+    const int64_t k0 = kt * kTileK + 32 * t + 8 * (lane >> 4);
+    uint32_t word = 0x88888888u;  // q = 0
+    if (col < n && k0 < k) word = plm_word_from_lsb_first(static_cast<uint32_t>(src[col * (k / 8) + k0 / 8]));
+    dst[idx] = word;
+}
+
+// One thread per dword of the fp8 layout: byte (((strip*KT + kt)*2 + h)*64 + lane)*16 + (t%2)*8 + i,
+// t = 2h + (dword%4)/2, i = 4*(dword%2) + 0..3.
+__global__ void repack_fp8_kernel(const uint8_t* __restrict__ src, uint32_t* __restrict__ dst, int64_t n, int64_t k,
+                                  int64_t ktiles, int64_t total) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int d = static_cast<int>(idx & 3);
+    const int lane = static_cast<int>((idx >> 2) & 63);
+    const int h = static_cast<int>((idx >> 8) & 1);
+    const int64_t tile = idx >> 9;
+    const int64_t kt = tile % ktiles;
+    const int64_t strip = tile / ktiles;
+    const int t = 2 * h + (d >> 1);
+    const int64_t col = strip * kTileN + (lane & 15);
+    const int64_t k0 = kt * kTileK + 32 * t + 8 * (lane >> 4) + 4 * (d & 1);
+    uint32_t word = 0;
+    if (col < n && k0 < k) {
+        const uint8_t* p = src + col * k + k0;
+        word = static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8) | (static_cast<uint32_t>(p[2]) << 16) |
+               (static_cast<uint32_t>(p[3]) << 24);
+    }
+    dst[idx] = word;
+}
+
+// Scales [ceil(N/bn), K/g] -> [strips][groups][cols], same element size; padding 0.
+template <typename T>
+__global__ void repack_scale_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t n, int64_t k,
+                                    int64_t block_n, int64_t group_size, int64_t groups, int cols, int64_t total) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int c = static_cast<int>(idx % cols);
+    const int64_t g = (idx / cols) % groups;
+    const int64_t strip = idx / (cols * groups);
+    const int64_t col = strip * kTileN + c;
+    const int64_t src_groups = k / group_size;
+    T v{};
+    if (col < n && g < src_groups) v = src[(col / block_n) * src_groups + g];
+    dst[idx] = v;
+}
+
+// Reference Marlin words -> plm int4 words. Marlin word index
+// ((cb*KTm + k/32)*8 + subtile)*32 + lane_m with lane_m = 4*(n%8) + pair holds,
+// in nibble j + 4*odd, K offset 2*pair + odd + 8j (marlin.cu:86-117).
+__global__ void convert_marlin_int4_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, int64_t n,
+                                           int64_t k, int64_t ktiles, int64_t total) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int t = static_cast<int>(idx & 3);
+    const int lane = static_cast<int>((idx >> 2) & 63);
+    const int64_t tile = idx >> 8;
+    const int64_t kt = tile % ktiles;
+    const int64_t strip = tile / ktiles;
+    const int64_t col = strip * kTileN + (lane & 15);
+    const int64_t k0 = kt * kTileK + 32 * t + 8 * (lane >> 4);
+    uint32_t word = 0x88888888u;
+    if (col < n && k0 < k) {
+        const int64_t ktm = ceil_div(k, 32);
+        const int64_t cb = col / 64, subtile = (col % 64) / 8;
+        word = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t kk = k0 + i;
+            const int c = static_cast<int>(kk % 32);
+            const int pair = (c % 8) / 2, odd = c % 2, j = c / 8;
+            const int lane_m = static_cast<int>(col % 8) * 4 + pair;
+            const uint32_t w = src[((cb * ktm + kk / 32) * 8 + subtile) * 32 + lane_m];
+            const uint32_t nib = (w >> (4 * (j + 4 * odd))) & 0xfu;  // already q ^ 8
+            const int pos = (i & 1) ? 4 + (i >> 1) : (i >> 1);
+            word |= nib << (4 * pos);
+        }
+    }
+    dst[idx] = word;
+}
+
+// Reference fp8 Marlin words -> plm fp8 layout. Word w of lane_m holds K offsets
+// 16w + 2*pair + {0, 1, 8, 9} in bytes 0..3 (marlin.cu:154-171).
+__global__ void convert_marlin_fp8_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, int64_t n,
+                                          int64_t k, int64_t ktiles, int64_t total) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int d = static_cast<int>(idx & 3);
+    const int lane = static_cast<int>((idx >> 2) & 63);
+    const int h = static_cast<int>((idx >> 8) & 1);
+    const int64_t tile = idx >> 9;
+    const int64_t kt = tile % ktiles;
+    const int64_t strip = tile / ktiles;
+    const int t = 2 * h + (d >> 1);
+    const int64_t col = strip * kTileN + (lane & 15);
+    const int64_t k0 = kt * kTileK + 32 * t + 8 * (lane >> 4) + 4 * (d & 1);
+    uint32_t word = 0;
+    if (col < n && k0 < k) {
+        const int64_t ktm = ceil_div(k, 32);
+        const int64_t cb = col / 64, subtile = (col % 64) / 8;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t kk = k0 + i;
+            const int c = static_cast<int>(kk % 32);
+            const int w = c / 16, cc = c % 16;
+            const int pair = (cc % 8) / 2, sub = (cc % 2) + 2 * (cc / 8);
+            const int lane_m = static_cast<int>(col % 8) * 4 + pair;
+            const uint32_t src_word = src[(((cb * ktm + kk / 32) * 8 + subtile) * 2 + w) * 32 + lane_m];
+            word |= ((src_word >> (8 * sub)) & 0xffu) << (8 * i);
+        }
+    }
+    dst[idx] = word;
+}
+
+// scale_marlin fp32 [groups, rows] (marlin.cu:227-236) -> plm fp32 [strips][groups][cols].
+__global__ void convert_marlin_scale_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t n,
+                                            int64_t k, int64_t block_n, int64_t group_size, int64_t groups, int cols,
+                                            int64_t total) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int c = static_cast<int>(idx % cols);
+    const int64_t g = (idx / cols) % groups;
+    const int64_t strip = idx / (cols * groups);
+    const int64_t col = strip * kTileN + c;
+    const int64_t rows = ceil_div(n, block_n);
+    float v = 0.f;
+    if (col < n && g < k / group_size) v = src[g * rows + col / block_n];
+    dst[idx] = v;
+}
+
+// Dense W[n, k] = round(q * round(scale)) in the output dtype, from the plm layout.
+template <plm_format F, bool BF16>
+__global__ void dequant_kernel(const uint8_t* __restrict__ w, const void* __restrict__ scale, int scale_dtype,
+                               int64_t n, int64_t k, int64_t ktiles, int64_t group_size, int64_t groups, int cols,
+                               uint16_t* __restrict__ out) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= n * k) return;
+    const int64_t row = idx / k, col_k = idx % k;
+    const int64_t strip = row / kTileN, kt = col_k / kTileK;
+    const int kin = static_cast<int>(col_k % kTileK);
+    const int t = kin / 32, kq = (kin % 32) / 8, i = kin % 8;
+    const int lane = static_cast<int>(row % kTileN) + 16 * kq;
+    float q;
+    if constexpr (F == PLM_INT4) {
+        const uint32_t word = reinterpret_cast<const uint32_t*>(w)[((strip * ktiles + kt) * 64 + lane) * 4 + t];
+        const int pos = (i & 1) ? 4 + (i >> 1) : (i >> 1);
+        q = static_cast<float>(static_cast<int>((word >> (4 * pos)) & 0xfu) - 8);
+    } else {
+        const int64_t off = ((strip * ktiles + kt) * 2 + t / 2) * 1024 + lane * 16 + (t % 2) * 8 + i;
+        q = e4m3_to_f32(w[off]);
+    }
+    const int64_t sidx = (strip * groups + col_k / group_size) * cols + (cols == 1 ? 0 : row % kTileN);
+    const float s = round_to<BF16>(load_scale(scale, sidx, scale_dtype));
+    out[idx] = static_cast<uint16_t>(to_bits16<BF16>(q * s));
+}
+
+constexpr int kThreads = 256;
+
+inline unsigned blocks_for(int64_t total) { return static_cast<unsigned>(ceil_div(total, kThreads)); }
+
+int check_common(const char* op, plm_dtype scale_dtype, int64_t n, int64_t k, int64_t block_n, int64_t group_size) {
+    PLM_CHECK_ARG(n >= 0 && k >= 0, op, "N and K must be non-negative");
+    PLM_CHECK_ARG(block_n > 0, op, "block_n must be positive");
+    PLM_CHECK_ARG(group_size > 0 && group_size % 16 == 0, op, "group_size must be a positive multiple of 16");
+    PLM_CHECK_ARG(k % group_size == 0, op, "K must be a multiple of group_size");
+    PLM_CHECK_ARG(scale_dtype == PLM_BF16 || scale_dtype == PLM_FP16 || scale_dtype == PLM_FP32, op,
+                  "scale dtype must be bf16, fp16 or fp32");
+    PLM_CHECK_ARG(n <= (int64_t{1} << 30) && k <= (int64_t{1} << 30), op, "N and K must be below 2^30");
+    return PLM_OK;
+}
+
+int launch_scale_repack(const char* op, const void* src, plm_dtype dt, int64_t n, int64_t k, int64_t block_n,
+                        int64_t group_size, void* dst, hipStream_t stream) {
+    const layout_dims d = make_dims(n, k, block_n, group_size);
+    const int64_t total = d.strips * d.groups * d.scale_cols;
+    if (total == 0) return PLM_OK;
+    if (dt == PLM_FP32) {
+        repack_scale_kernel<uint32_t><<<blocks_for(total), kThreads, 0, stream>>>(
+            static_cast<const uint32_t*>(src), static_cast<uint32_t*>(dst), n, k, block_n, group_size, d.groups,
+            d.scale_cols, total);
+    } else {
+        repack_scale_kernel<uint16_t><<<blocks_for(total), kThreads, 0, stream>>>(
+            static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), n, k, block_n, group_size, d.groups,
+            d.scale_cols, total);
+    }
+    PLM_HIP_LAUNCH_CHECK(op);
+    return PLM_OK;
+}
+
+}  // namespace
+}  // namespace plm
+
+using namespace plm;
+
+extern "C" {
+
+const char* plm_last_error(void) { return g_error.c_str(); }
+
+const char* plm_version(void) { return "pulsarlm_amd 0.1 gfx950"; }
+
+int64_t plm_weight_bytes(plm_format format, int64_t n, int64_t k) {
+    if (n < 0 || k < 0 || (format != PLM_INT4 && format != PLM_FP8)) return -1;
+    return ceil_div(n, kTileN) * ceil_div(k, kTileK) * tile_bytes(format);
+}
+
+int64_t plm_scale_bytes(int64_t n, int64_t k, int64_t block_n, int64_t group_size, plm_dtype scale_dtype) {
+    if (n < 0 || k < 0 || block_n <= 0 || group_size <= 0 || group_size % 16 != 0) return -1;
+    if (scale_dtype != PLM_BF16 && scale_dtype != PLM_FP16 && scale_dtype != PLM_FP32) return -1;
+    const layout_dims d = make_dims(n, k, block_n, group_size);
+    return d.strips * d.groups * d.scale_cols * dtype_size(scale_dtype);
+}
+
+int plm_repack_int4(const int32_t* weight_packed, const void* weight_scale, plm_dtype scale_dtype, int64_t n,
+                    int64_t k, int64_t block_n, int64_t group_size, void* weight_out, void* scale_out,
+                    void* stream) {
+    const char* op = "repack_int4_marlin";
+    clear_error();
+    if (int rc = check_common(op, scale_dtype, n, k, block_n, group_size)) return rc;
+    PLM_CHECK_ARG(k % 8 == 0, op, "K must be a multiple of 8");
+    const int64_t total = ceil_div(n, kTileN) * ceil_div(k, kTileK) * 256;
+    PLM_CHECK_ARG(total == 0 || (weight_packed && weight_out && weight_scale && scale_out), op, "null pointer");
+    PLM_CHECK_ARG(aligned(weight_out, 16), op, "weight_out must be 16-byte aligned");
+    hipStream_t s = as_stream(stream);
+    if (total > 0) {
+        repack_int4_kernel<<<blocks_for(total), kThreads, 0, s>>>(weight_packed, static_cast<uint32_t*>(weight_out),
+                                                                  n, k, ceil_div(k, kTileK), total);
+        PLM_HIP_LAUNCH_CHECK(op);
+    }
+    return launch_scale_repack(op, weight_scale, scale_dtype, n, k, block_n, group_size, scale_out, s);
+}
+
+int plm_repack_fp8(const uint8_t* weight, const void* weight_scale, plm_dtype scale_dtype, int64_t n, int64_t k,
+                   int64_t block_n, int64_t group_size, void* weight_out, void* scale_out, void* stream) {
+    const char* op = "repack_fp8_marlin";
+    clear_error();
+    if (int rc = check_common(op, scale_dtype, n, k, block_n, group_size)) return rc;
+    const int64_t total = ceil_div(n, kTileN) * ceil_div(k, kTileK) * 512;
+    PLM_CHECK_ARG(total == 0 || (weight && weight_out && weight_scale && scale_out), op, "null pointer");
+    PLM_CHECK_ARG(aligned(weight_out, 16), op, "weight_out must be 16-byte aligned");
+    hipStream_t s = as_stream(stream);
+    if (total > 0) {
+        repack_fp8_kernel<<<blocks_for(total), kThreads, 0, s>>>(weight, static_cast<uint32_t*>(weight_out), n, k,
+                                                                 ceil_div(k, kTileK), total);
+        PLM_HIP_LAUNCH_CHECK(op);
+    }
+    return launch_scale_repack(op, weight_scale, scale_dtype, n, k, block_n, group_size, scale_out, s);
+}
+
+int plm_convert_marlin(plm_format format, const int32_t* weight_marlin, const float* scale_marlin, int64_t n,
+                       int64_t k, int64_t block_n, int64_t group_size, void* weight_out, void* scale_out,
+                       void* stream) {
+    const char* op = "convert_marlin";
+    clear_error();
+    if (int rc = check_common(op, PLM_FP32, n, k, block_n, group_size)) return rc;
+    PLM_CHECK_ARG(format == PLM_INT4 || format == PLM_FP8, op, "unknown format");
+    hipStream_t s = as_stream(stream);
+    const int64_t ktiles = ceil_div(k, kTileK);
+    const int64_t total = ceil_div(n, kTileN) * ktiles * (format == PLM_INT4 ? 256 : 512);
+    PLM_CHECK_ARG(total == 0 || (weight_marlin && weight_out && scale_marlin && scale_out), op, "null pointer");
+    if (total > 0) {
+        if (format == PLM_INT4) {
+            convert_marlin_int4_kernel<<<blocks_for(total), kThreads, 0, s>>>(
+                reinterpret_cast<const uint32_t*>(weight_marlin), static_cast<uint32_t*>(weight_out), n, k, ktiles,
+                total);
+        } else {
+            convert_marlin_fp8_kernel<<<blocks_for(total), kThreads, 0, s>>>(
+                reinterpret_cast<const uint32_t*>(weight_marlin), static_cast<uint32_t*>(weight_out), n, k, ktiles,
+                total);
+        }
+        PLM_HIP_LAUNCH_CHECK(op);
+    }
+    const layout_dims d = make_dims(n, k, block_n, group_size);
+    const int64_t stotal = d.strips * d.groups * d.scale_cols;
+    if (stotal > 0) {
+        convert_marlin_scale_kernel<<<blocks_for(stotal), kThreads, 0, s>>>(
+            scale_marlin, static_cast<float*>(scale_out), n, k, block_n, group_size, d.groups, d.scale_cols, stotal);
+        PLM_HIP_LAUNCH_CHECK(op);
+    }
+    return PLM_OK;
+}
+
+int plm_dequant(plm_format format, const void* weight, const void* scale, plm_dtype scale_dtype, int64_t n, int64_t k,
+                int64_t block_n, int64_t group_size, void* out, plm_dtype out_dtype, void* stream) {
+    const char* op = "dequant";
+    clear_error();
+    if (int rc = check_common(op, scale_dtype, n, k, block_n, group_size)) return rc;
+    PLM_CHECK_ARG(format == PLM_INT4 || format == PLM_FP8, op, "unknown format");
+    PLM_CHECK_ARG(out_dtype == PLM_BF16 || out_dtype == PLM_FP16, op, "out dtype must be bf16 or fp16");
+    const int64_t total = n * k;
+    if (total == 0) return PLM_OK;
+    PLM_CHECK_ARG(weight && scale && out, op, "null pointer");
+    const layout_dims d = make_dims(n, k, block_n, group_size);
+    hipStream_t s = as_stream(stream);
+    auto w8 = static_cast<const uint8_t*>(weight);
+    auto o = static_cast<uint16_t*>(out);
+    const bool bf = out_dtype == PLM_BF16;
+    if (format == PLM_INT4) {
+        if (bf)
+            dequant_kernel<PLM_INT4, true><<<blocks_for(total), kThreads, 0, s>>>(
+                w8, scale, scale_dtype, n, k, d.ktiles, group_size, d.groups, d.scale_cols, o);
+        else
+            dequant_kernel<PLM_INT4, false><<<blocks_for(total), kThreads, 0, s>>>(
+                w8, scale, scale_dtype, n, k, d.ktiles, group_size, d.groups, d.scale_cols, o);
+    } else {
+        if (bf)
+            dequant_kernel<PLM_FP8, true><<<blocks_for(total), kThreads, 0, s>>>(
+                w8, scale, scale_dtype, n, k, d.ktiles, group_size, d.groups, d.scale_cols, o);
+        else
+            dequant_kernel<PLM_FP8, false><<<blocks_for(total), kThreads, 0, s>>>(
+                w8, scale, scale_dtype, n, k, d.ktiles, group_size, d.groups, d.scale_cols, o);
+    }
+    PLM_HIP_LAUNCH_CHECK(op);
+    return PLM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,197 @@
+"""Tensor-level ops over the C ABI, mirroring pulsarlm-core's quant-linear ops.
+
+Same names, argument meaning and error behaviour as the reference's
+``pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:299-343``:
+
+* ``repack_int4_marlin_cuda(weight_packed, weight_scale, block_n, group_size)``
+  -> ``(weight_marlin, scale_marlin)``
+* ``repack_fp8_marlin_cuda(weight, weight_scale, block_n, group_size)``
+* ``gemm_int4_marlin_cuda(x, weight_marlin, scale_marlin, n, block_n, group_size)``
+* ``gemm_fp8_marlin_cuda(...)``
+
+``weight_marlin`` is an opaque 1-D int32 tensor in the plm tile layout (the
+reference's is also opaque, marlin.cu:21-30); ``scale_marlin`` keeps the scale's
+source dtype, shaped [strips, groups, cols]. Errors raise ``RuntimeError`` with
+the reference's ``"<op>: ..."`` message style. Work is enqueued on torch's
+current stream of the tensors' device; nothing synchronizes.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.PLM_BF16, torch.float16: _lib.PLM_FP16, torch.float32: _lib.PLM_FP32}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require(cond: bool, op: str, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(f"{op}: {msg}")
+
+
+def _call(fn_name: str, *args) -> None:
+    lib = _lib.load()
+    _lib.check(getattr(lib, fn_name)(*args))
+
+
+# ---------------------------------------------------------------------------
+# Workspace: one zero-initialised buffer per (device, stream). The kernels leave
+# their arrival counters at zero, so reuse by calls ordered on one stream is safe.
+# ---------------------------------------------------------------------------
+_ws_lock = threading.Lock()
+_ws: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    if nbytes <= 0:
+        return None
+    key = (device.index if device.index is not None else torch.cuda.current_device(), _stream(device))
+    with _ws_lock:
+        buf = _ws.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 1 << 20)
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            _ws[key] = buf
+        return buf
+
+
+# ---------------------------------------------------------------------------
+# Repack
+# ---------------------------------------------------------------------------
+
+
+def _scale_shape(n: int, k: int, block_n: int, group_size: int):
+    strips = -(-n // 16)
+    ktiles = -(-k // 128)
+    groups = -(-(ktiles * 128) // group_size)
+    cols = 1 if block_n % 16 == 0 else 16
+    return strips, groups, cols
+
+
+def _repack(op: str, fmt: int, weight: torch.Tensor, n: int, k: int, weight_scale: torch.Tensor, block_n: int,
+            group_size: int):
+    _require(weight.is_cuda and weight_scale.is_cuda, op, "inputs must be CUDA tensors")
+    _require(block_n > 0, op, "block_n must be positive")
+    _require(group_size > 0 and group_size % 16 == 0, op, "group_size must be a positive multiple of 16")
+    _require(k % group_size == 0, op, "K must be a multiple of group_size")
+    rows = -(-n // block_n)
+    _require(weight_scale.dim() == 2 and tuple(weight_scale.shape) == (rows, k // group_size), op,
+             "weight_scale must be [ceil(N / block_n), K / group_size]")
+    _require(weight_scale.dtype in _DTYPES, op, "weight_scale must be fp32, fp16 or bf16")
+    src = weight.contiguous()
+    scale = weight_scale.contiguous()
+    lib = _lib.load()
+    wbytes = lib.plm_weight_bytes(fmt, n, k)
+    w_out = torch.empty(max(wbytes // 4, 0), dtype=torch.int32, device=weight.device)
+    s_out = torch.empty(_scale_shape(n, k, block_n, group_size), dtype=scale.dtype, device=weight.device)
+    fn = "plm_repack_int4" if fmt == _lib.PLM_INT4 else "plm_repack_fp8"
+    with torch.cuda.device(weight.device):
+        _call(fn, _ptr(src), _ptr(scale), _DTYPES[scale.dtype], n, k, block_n, group_size, _ptr(w_out), _ptr(s_out),
+              _stream(weight.device))
+    return w_out, s_out
+
+
+def repack_int4_marlin_cuda(weight_packed: torch.Tensor, weight_scale: torch.Tensor, block_n: int, group_size: int):
+    """int32 [N, K/8] LSB-first int4 + scales [ceil(N/bn), K/g] -> (weight, scale) in the plm layout
+    (ops.hpp:317-322; marlin.cu:601-620)."""
+    _require(weight_packed.dtype == torch.int32 and weight_packed.dim() == 2, "repack_int4_marlin",
+             "weight_packed must be int32 [N, K/8]")
+    n, k = weight_packed.shape[0], weight_packed.shape[1] * 8
+    return _repack("repack_int4_marlin", _lib.PLM_INT4, weight_packed, n, k, weight_scale, block_n, group_size)
+
+
+def repack_fp8_marlin_cuda(weight: torch.Tensor, weight_scale: torch.Tensor, block_n: int, group_size: int):
+    """float8_e4m3fn [N, K] + scales -> (weight, scale) in the plm layout (ops.hpp:324-325; marlin.cu:622-629)."""
+    _require(weight.dtype == torch.float8_e4m3fn and weight.dim() == 2, "repack_fp8_marlin",
+             "weight must be float8_e4m3fn [N, K]")
+    n, k = weight.shape
+    return _repack("repack_fp8_marlin", _lib.PLM_FP8, weight.view(torch.uint8), n, k, weight_scale, block_n,
+                   group_size)
+
+
+def convert_marlin_cuda(fmt: str, weight_marlin: torch.Tensor, scale_marlin: torch.Tensor, n: int, k: int,
+                        block_n: int, group_size: int):
+    """Reference Marlin (words, fp32 [K/g, ceil(N/bn)] scales) -> plm layout (fp32 scales)."""
+    op = "convert_marlin"
+    f = _lib.PLM_INT4 if fmt == "int4" else _lib.PLM_FP8
+    _require(weight_marlin.dtype == torch.int32 and scale_marlin.dtype == torch.float32, op,
+             "weight_marlin must be int32 and scale_marlin fp32")
+    lib = _lib.load()
+    w_out = torch.empty(lib.plm_weight_bytes(f, n, k) // 4, dtype=torch.int32, device=weight_marlin.device)
+    s_out = torch.empty(_scale_shape(n, k, block_n, group_size), dtype=torch.float32, device=weight_marlin.device)
+    with torch.cuda.device(weight_marlin.device):
+        _call("plm_convert_marlin", f, _ptr(weight_marlin.contiguous()), _ptr(scale_marlin.contiguous()), n, k,
+              block_n, group_size, _ptr(w_out), _ptr(s_out), _stream(weight_marlin.device))
+    return w_out, s_out
+
+
+def dequant_marlin_cuda(fmt: str, weight_marlin: torch.Tensor, scale_marlin: torch.Tensor, n: int, k: int,
+                        block_n: int, group_size: int, dtype=torch.bfloat16) -> torch.Tensor:
+    """Dense [N, K] round(q * round(scale)) in ``dtype`` from the plm layout."""
+    f = _lib.PLM_INT4 if fmt == "int4" else _lib.PLM_FP8
+    out = torch.empty((n, k), dtype=dtype, device=weight_marlin.device)
+    with torch.cuda.device(weight_marlin.device):
+        _call("plm_dequant", f, _ptr(weight_marlin), _ptr(scale_marlin), _DTYPES[scale_marlin.dtype], n, k, block_n,
+              group_size, _ptr(out), _DTYPES[dtype], _stream(weight_marlin.device))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+
+
+def _gemm_checks(op: str, fmt: int, x: torch.Tensor, weight_marlin: torch.Tensor, scale_marlin: torch.Tensor, n: int,
+                 block_n: int, group_size: int):
+    """gemm<fmt> checks, marlin.cu:547-571."""
+    _require(x.is_cuda and weight_marlin.is_cuda and scale_marlin.is_cuda, op, "all inputs must be CUDA tensors")
+    _require(x.dtype in (torch.float16, torch.bfloat16), op, "x must be fp16 or bf16")
+    _require(x.dim() == 2 and x.is_contiguous(), op, "x must be a contiguous [M, K]")
+    _require(weight_marlin.dtype == torch.int32, op, "weight_marlin must be int32")
+    _require(scale_marlin.dtype in _DTYPES, op, "scale_marlin must be fp32, fp16 or bf16")
+    _require(block_n > 0, op, "block_n must be positive")
+    _require(group_size > 0 and group_size % 16 == 0, op, "group_size must be a positive multiple of 16")
+    k = x.shape[1]
+    _require(k % group_size == 0, op, "K must be a multiple of group_size")
+    _require(tuple(scale_marlin.shape) == _scale_shape(n, k, block_n, group_size), op,
+             "scale_marlin has the wrong shape for this N, K, block_n and group_size")
+    _require(weight_marlin.numel() * 4 == _lib.load().plm_weight_bytes(fmt, n, k), op,
+             "weight_marlin has the wrong size for this shape")
+
+
+def _gemm(op: str, fmt: int, x, weight_marlin, scale_marlin, n: int, block_n: int, group_size: int,
+          out: torch.Tensor | None = None) -> torch.Tensor:
+    _gemm_checks(op, fmt, x, weight_marlin, scale_marlin, n, block_n, group_size)
+    m, k = x.shape
+    y = out if out is not None else torch.empty((m, n), dtype=x.dtype, device=x.device)
+    if m == 0 or n == 0:
+        return y
+    lib = _lib.load()
+    wsb = lib.plm_gemm_workspace_bytes(fmt, m, n, k)
+    ws = workspace(x.device, wsb)
+    with torch.cuda.device(x.device):
+        _call("plm_gemm", fmt, _ptr(x), _DTYPES[x.dtype], _ptr(weight_marlin.contiguous()),
+              _ptr(scale_marlin.contiguous()), _DTYPES[scale_marlin.dtype], m, n, k, block_n, group_size, _ptr(y),
+              _ptr(ws), 0 if ws is None else ws.numel(), _stream(x.device))
+    return y
+
+
+def gemm_int4_marlin_cuda(x, weight_marlin, scale_marlin, n: int, block_n: int, group_size: int, out=None):
+    """y [M, N] = x [M, K] @ dequant(W)^T (ops.hpp:327-334; marlin.cu:631-640)."""
+    return _gemm("gemm_int4_marlin", _lib.PLM_INT4, x, weight_marlin, scale_marlin, n, block_n, group_size, out)
+
+
+def gemm_fp8_marlin_cuda(x, weight_marlin, scale_marlin, n: int, block_n: int, group_size: int, out=None):
+    """fp8 W8A16 form (ops.hpp:336-343; marlin.cu:642-651)."""
+    return _gemm("gemm_fp8_marlin", _lib.PLM_FP8, x, weight_marlin, scale_marlin, n, block_n, group_size, out)

@@ -1,0 +1,202 @@
+"""Parity of the HIP W4A16 / W8A16 path with the CPU oracle, through the C ABI.
+
+Mirrors pulsarlm-core/tests/kernels/test_marlin.cpp (shape n=200, k=144, g=16;
+identity-GEMM exactness; dequantize-then-matmul tolerance) and extends it to the
+BASELINE configs. Tolerance for every GEMM: elementwise |y - ref| <= 2e-2 +
+2e-2 |ref| (the reference's allclose, test_marlin.cpp:95,113) and rel-L2 <= 5e-3
+against the float64-accumulated dequantize-then-matmul of the reference's
+dequantized weights."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from pulsarlm_amd import ops
+from tests._util import TDT, assert_close, fp8_case, int4_case, scale_tensor, to_dev, to_np, x_case
+
+pytestmark = pytest.mark.gpu
+
+N, K, G = 200, 144, 16  # test_marlin.cpp:15-17
+
+
+def _repack_int4(packed, scale, block_n, g):
+    return ops.repack_int4_marlin_cuda(to_dev(packed), scale_tensor(scale), block_n, g)
+
+
+def _repack_fp8(codes, scale, block_n, g):
+    w = to_dev(codes).view(torch.float8_e4m3fn)
+    return ops.repack_fp8_marlin_cuda(w, scale_tensor(scale), block_n, g)
+
+
+# ------------------------------------------------------------------ repack / dequant
+
+
+@pytest.mark.parametrize("block_n", [1, 128])
+@pytest.mark.parametrize("sdt", [np.float16, np.float32])
+def test_repack_int4_bit_exact(block_n, sdt):
+    packed, s = int4_case(N, K, G, block_n, seed=1, scale_dtype=sdt, scale_kind="test")
+    w, sc = _repack_int4(packed, s, block_n, G)
+    torch.cuda.synchronize()
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), O.plm_layout_int4(packed))
+    assert np.array_equal(sc.cpu().numpy(), O.plm_layout_scale(s, N, K, block_n, G))
+
+
+@pytest.mark.parametrize("block_n", [1, 128])
+def test_repack_fp8_bit_exact(block_n):
+    codes, s = fp8_case(N, K, G, block_n, seed=2)
+    w, sc = _repack_fp8(codes, s, block_n, G)
+    assert np.array_equal(w.cpu().numpy().view(np.uint8), O.plm_layout_fp8(codes))
+    assert np.array_equal(sc.cpu().numpy(), O.plm_layout_scale(s, N, K, block_n, G))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("block_n", [1, 128])
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+def test_dequant_bit_exact(fmt, dtype, block_n):
+    if fmt == "int4":
+        packed, s = int4_case(N, K, G, block_n, seed=3, scale_dtype=np.float32, scale_kind="test")
+        w, sc = _repack_int4(packed, s, block_n, G)
+        ref = O.dequant_int4(packed, s, block_n, G, dtype)
+    else:
+        codes, s = fp8_case(N, K, G, block_n, seed=3)
+        w, sc = _repack_fp8(codes, s, block_n, G)
+        ref = O.dequant_fp8(codes, s, block_n, G, dtype)
+    got = ops.dequant_marlin_cuda(fmt, w, sc, N, K, block_n, G, TDT[dtype])
+    assert np.array_equal(to_np(got), ref)
+
+
+# ------------------------------------------------------------------ identity GEMM (exactness)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("block_n", [1, 128])
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+@pytest.mark.parametrize("g", [16, 48, 32, 128])
+def test_identity_gemm_exact(fmt, dtype, block_n, g):
+    """test_marlin.cpp:54-78: y = I_k @ dequant(W)^T must equal dequant(W)^T exactly,
+    through the MFMA path (M = K) and the decode path (16-row and 1-row slices)."""
+    n, k = N, 144 if g in (16, 48) else 256
+    if fmt == "int4":
+        packed, s = int4_case(n, k, g, block_n, seed=4, scale_dtype=np.float32, scale_kind="test")
+        w, sc = _repack_int4(packed, s, block_n, g)
+        ref = O.dequant_int4(packed, s, block_n, g, dtype)
+        gemm = ops.gemm_int4_marlin_cuda
+    else:
+        codes, s = fp8_case(n, k, g, block_n, seed=4)
+        w, sc = _repack_fp8(codes, s, block_n, g)
+        ref = O.dequant_fp8(codes, s, block_n, g, dtype)
+        gemm = ops.gemm_fp8_marlin_cuda
+    eye = torch.eye(k, dtype=TDT[dtype], device="cuda")
+    y = gemm(eye, w, sc, n, block_n, g)
+    assert np.array_equal(to_np(y), ref.T), "MFMA path"
+    for r0, rows in [(0, 16), (k - 16, 16), (37, 1), (70, 5)]:
+        y = gemm(eye[r0:r0 + rows].contiguous(), w, sc, n, block_n, g)
+        assert np.array_equal(to_np(y), ref.T[r0:r0 + rows]), f"decode path rows {r0}+{rows}"
+
+
+# ------------------------------------------------------------------ dequantize-then-matmul tolerance
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 100, 300])
+def test_int4_gemm_reference_shape(m, dtype):
+    """test_marlin.cpp:98-114 (block_n = 1)."""
+    packed, s = int4_case(N, K, G, 1, seed=5, scale_dtype=np.float32, scale_kind="test")
+    w, sc = _repack_int4(packed, s, 1, G)
+    x = x_case(m, K, dtype, seed=m)
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, TDT[dtype]), w, sc, N, 1, G)
+    assert y.shape == (m, N) and y.dtype == TDT[dtype]
+    assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, G, dtype), None), f"m={m}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("m", [1, 16, 100])
+def test_fp8_gemm_reference_shape(m, dtype):
+    """test_marlin.cpp:80-96 (block_n = 128)."""
+    codes, s = fp8_case(N, K, G, 128, seed=6)
+    w, sc = _repack_fp8(codes, s, 128, G)
+    x = x_case(m, K, dtype, seed=m)
+    y = ops.gemm_fp8_marlin_cuda(to_dev(x, TDT[dtype]), w, sc, N, 128, G)
+    assert_close(y, O.gemm_ref(x, O.dequant_fp8(codes, s, 128, G, dtype), None), f"m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 64, 256])
+@pytest.mark.parametrize("g", [32, 64, 128, 256])
+def test_int4_gemm_group_sizes(m, g):
+    n, k = 520, 1024
+    packed, s = int4_case(n, k, g, 1, seed=g)
+    w, sc = _repack_int4(packed, s, 1, g)
+    x = x_case(m, k, "bf16", seed=m + g)
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, torch.bfloat16), w, sc, n, 1, g)
+    assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, g), None), f"m={m} g={g}")
+
+
+def test_config1_m16_k4096_n4096():
+    """M=16, K=N=4096, int4 g128 symmetric, fp16 scales |N(0,.02)|+1e-3."""
+    x, packed, s = O.make_w4a16(16, 4096, 4096, 128, seed=1)
+    w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), to_dev(s), 1, 128)
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, torch.bfloat16), w, sc, 4096, 1, 128)
+    st = assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, 128), None), "config1")
+    print("config1", st)
+
+
+@pytest.mark.parametrize("shape", [(4096, 6144), (4096, 4096), (4096, 24576), (12288, 4096)])
+@pytest.mark.parametrize("m", [1, 4, 16, 256])
+def test_qwen3_8b_shapes(shape, m):
+    k, n = shape
+    x, packed, s = O.make_w4a16(m, n, k, 128, seed=k + n + m)
+    w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), to_dev(s), 1, 128)
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, torch.bfloat16), w, sc, n, 1, 128)
+    assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, 128), None), f"{shape} m={m}")
+
+
+def test_deterministic_across_calls():
+    x, packed, s = O.make_w4a16(16, 4096, 12288, 128, seed=9)
+    w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), to_dev(s), 1, 128)
+    xd = to_dev(x, torch.bfloat16)
+    a = ops.gemm_int4_marlin_cuda(xd, w, sc, 4096, 1, 128)
+    b = ops.gemm_int4_marlin_cuda(xd, w, sc, 4096, 1, 128)
+    assert torch.equal(a, b)
+    x2 = to_dev(O.make_w4a16(300, 64, 12288, 128, seed=9)[0], torch.bfloat16)
+    a = ops.gemm_int4_marlin_cuda(x2, w, sc, 4096, 1, 128)
+    b = ops.gemm_int4_marlin_cuda(x2, w, sc, 4096, 1, 128)
+    assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ Marlin-layout ingest, edge cases
+
+
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+def test_convert_marlin_matches_repack(fmt):
+    bn = 1 if fmt == "int4" else 128
+    if fmt == "int4":
+        packed, s = int4_case(N, K, G, bn, seed=7, scale_dtype=np.float32, scale_kind="test")
+        words = O.marlin_encode_int4(packed)
+        w_ref, s_ref = _repack_int4(packed, s, bn, G)
+    else:
+        codes, s = fp8_case(N, K, G, bn, seed=7)
+        words = O.marlin_encode_fp8(codes)
+        w_ref, s_ref = _repack_fp8(codes, s, bn, G)
+    w, sc = ops.convert_marlin_cuda(fmt, to_dev(words), to_dev(O.marlin_scale(s)), N, K, bn, G)
+    assert torch.equal(w, w_ref)
+    assert torch.equal(sc, s_ref)
+
+
+def test_empty_m_and_n():
+    packed, s = int4_case(N, K, G, 1, seed=8, scale_dtype=np.float32)
+    w, sc = _repack_int4(packed, s, 1, G)
+    y = ops.gemm_int4_marlin_cuda(torch.empty((0, K), dtype=torch.bfloat16, device="cuda"), w, sc, N, 1, G)
+    assert y.shape == (0, N)
+
+
+def test_errors_name_the_op():
+    packed, s = int4_case(N, K, G, 1, seed=8, scale_dtype=np.float32)
+    w, sc = _repack_int4(packed, s, 1, G)
+    x = torch.zeros((4, K), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(RuntimeError, match="gemm_int4_marlin: .*wrong size"):
+        ops.gemm_int4_marlin_cuda(x, w[:-1], sc, N, 1, G)
+    with pytest.raises(RuntimeError, match="gemm_int4_marlin: x must be fp16 or bf16"):
+        ops.gemm_int4_marlin_cuda(x.float(), w, sc, N, 1, G)
+    with pytest.raises(RuntimeError, match="repack_int4_marlin: group_size"):
+        ops.repack_int4_marlin_cuda(to_dev(packed), scale_tensor(s), 1, 24)

@@ -1,0 +1,307 @@
+"""Pins for the CPU oracle (oracle/oracle.py): each restated function is checked
+against an independent library routine, a closed form, hand-derived known
+answers, or an invariant, so a dropped term / wrong index / wrong rounding
+fails here. CPU only."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+
+# ---------------------------------------------------------------- scalar formats
+
+
+def _sweep_f32(rng, n=200_000):
+    v = rng.standard_normal(n).astype(np.float32) * np.exp2(rng.integers(-30, 30, n)).astype(np.float32)
+    # Exact ties for bf16: low 16 bits = 0x8000, both parities of bit 16.
+    ties = (rng.integers(0, 2**31, 4000, dtype=np.uint32) & ~np.uint32(0xFFFF)) | np.uint32(0x8000)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, 1e-40, -1e-40, 3.4e38, 65504.0, 65520.0, 6e-8, 1.0, -1.0],
+                       dtype=np.float32)
+    return np.concatenate([v, ties.view(np.float32), special])
+
+
+def test_bf16_round_matches_torch():
+    v = _sweep_f32(np.random.default_rng(0))
+    got = O.bf16_round(v)
+    ref = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+    nan = np.isnan(ref)  # NaN payloads may differ; NaN-ness may not
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_fp16_round_matches_torch():
+    v = _sweep_f32(np.random.default_rng(1))
+    got = O.fp16_round(v)
+    ref = torch.from_numpy(v).to(torch.float16).float().numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_e4m3_decode_all_codes_match_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    got = O.e4m3_decode(codes)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert nan.sum() == 2 and nan[0x7F] and nan[0xFF]
+    assert np.array_equal(got[~nan], ref[~nan])
+    # Closed-form spot checks: max normal, min subnormal, one.
+    assert got[0x7E] == 448.0 and got[0x01] == 2.0**-9 and got[0x38] == 1.0 and got[0xB8] == -1.0
+
+
+def test_e4m3_encode_matches_torch():
+    rng = np.random.default_rng(2)
+    v = np.concatenate([
+        rng.standard_normal(100_000).astype(np.float32) * 100,
+        rng.standard_normal(20_000).astype(np.float32) * 1e-2,
+        O.e4m3_decode(np.arange(0x7F, dtype=np.uint8)),  # exact grid points
+        (O.e4m3_decode(np.arange(0x7E, dtype=np.uint8)) + O.e4m3_decode(np.arange(1, 0x7F, dtype=np.uint8))) / 2,
+        np.array([448, 460, 464, 465, 479, 480, 500, -470, 2**-10, 3 * 2**-10], dtype=np.float32),
+    ]).astype(np.float32)
+    got = O.e4m3_encode(v)
+    ref = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    # torch maps NaN codes with either sign bit; compare values where not NaN, NaN-ness where NaN.
+    gn = (got & 0x7F) == 0x7F
+    rn = (ref & 0x7F) == 0x7F
+    assert np.array_equal(gn, rn)
+    assert np.array_equal(got[~gn], ref[~rn])
+
+
+# ---------------------------------------------------------------- int4 packing
+
+
+def test_pack_int4_known_answer():
+    q = np.array([[1, 2, 3, 4, 5, 6, 7, -8], [-1, 0, 0, 0, 0, 0, 0, 0]])
+    words = O.pack_int4(q).view(np.uint32)
+    assert words[0, 0] == 0x87654321
+    assert words[1, 0] == 0x0000000F
+    assert np.array_equal(O.unpack_int4(O.pack_int4(q)), q)
+
+
+def test_unpack_every_nibble():
+    for v in range(16):
+        word = np.array([[v << 28]], dtype=np.uint32).view(np.int32)
+        q = O.unpack_int4(word)
+        assert q[0, 7] == (v if v < 8 else v - 16)
+        assert np.all(q[0, :7] == 0)
+
+
+# ---------------------------------------------------------------- dequant
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_dequant_int4_matches_reference_expression(dtype):
+    """Every nibble x a scale sweep against test_marlin.cpp:48-50 evaluated by ATen:
+    weight.to(dtype) * expanded_scale.to(dtype)."""
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    rng = np.random.default_rng(3)
+    n, k, g = 64, 16 * 16, 16
+    q = np.tile(np.arange(-8, 8), (n, k // 16))
+    scale = (rng.random((n, k // g)).astype(np.float32) * 0.1 + 0.01).astype(np.float32)
+    scale[0, :] = np.float32(1.0 / 3.0)
+    scale[1, :] = np.float32(2.0 ** -20)
+    got = O.dequant_int4(O.pack_int4(q), scale, 1, g, dtype)
+    expanded = torch.from_numpy(scale).repeat_interleave(g, 1)
+    ref = (torch.from_numpy(q).to(tdt) * expanded.to(tdt)).float().numpy()
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("block_n", [1, 128])
+def test_dequant_fp8_matches_reference_expression(dtype, block_n):
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    rng = np.random.default_rng(4)
+    n, k, g = 200, 144, 16
+    codes = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    codes[(codes == 0x7F) | (codes == 0xFF)] = 0
+    scale = (rng.random((-(-n // block_n), k // g)).astype(np.float32) * 0.1 + 0.01)
+    got = O.dequant_fp8(codes, scale, block_n, g, dtype)
+    w = torch.from_numpy(codes).view(torch.float8_e4m3fn)
+    exp = torch.from_numpy(scale).repeat_interleave(block_n, 0)[:n].repeat_interleave(g, 1)
+    ref = (w.to(tdt) * exp.to(tdt)).float().numpy()
+    assert np.array_equal(got, ref)
+
+
+def test_dequant_plain_int4_rounds_once():
+    """int4_gemm.cu:136-138 rounds q * fp32 scale once; differs from the Marlin rounding."""
+    q = np.full((1, 8), 7)
+    scale = np.array([[np.float32(0.1)]], dtype=np.float32)
+    plain = O.dequant_int4_plain(O.pack_int4(q), np.repeat(scale, 1, axis=1), 8, "bf16")
+    ref = torch.tensor(7.0 * np.float32(0.1), dtype=torch.float32).to(torch.bfloat16).float().item()
+    assert plain[0, 0] == ref
+
+
+# ---------------------------------------------------------------- Marlin layout
+
+
+def test_marlin_int4_known_word():
+    """marlin.cu:21-30,86-88: lane L holds column L/4 of its 8-column subtile; its
+    nibbles are K offsets 2p+{0,8,16,24} then 2p+1+{0,8,16,24}, p = L%4, stored as q^8."""
+    n, k = 64, 32
+    q = np.zeros((n, k), dtype=np.int64)
+    # Column-block 0, subtile 1 (rows 8..15), lane 6 -> row 8 + 1 = 9, pair 2.
+    offs = [4, 12, 20, 28, 5, 13, 21, 29]
+    vals = [1, 2, 3, -1, -2, -3, 7, -8]
+    for o, v in zip(offs, vals):
+        q[9, o] = v
+    words = O.marlin_encode_int4(O.pack_int4(q)).view(np.uint32)
+    w = int(words[(0 * 8 + 1) * 32 + 6])
+    expect = 0
+    for p, v in enumerate(vals):
+        expect |= ((v & 0xF) ^ 8) << (4 * p)
+    assert w == expect
+    # A lane with all-zero weights reads 0x88888888.
+    assert int(words[0]) == 0x88888888
+
+
+def test_marlin_fp8_known_word():
+    """marlin.cu:154-155: word w of lane L holds K offsets 16w + 2p + {0, 1, 8, 9}."""
+    n, k = 64, 32
+    c = np.zeros((n, k), dtype=np.uint8)
+    # subtile 0, lane 13 -> row 3, pair 1; word 1 -> K 16 + 2 + {0,1,8,9} = 18, 19, 26, 27.
+    for o, v in zip([18, 19, 26, 27], [0x11, 0x22, 0x33, 0x44]):
+        c[3, o] = v
+    words = O.marlin_encode_fp8(c).view(np.uint32)
+    assert int(words[(0 * 2 + 1) * 32 + 13]) == 0x44332211
+
+
+@pytest.mark.parametrize("n,k", [(200, 144), (64, 32), (7, 96), (130, 1024)])
+def test_marlin_round_trip(n, k):
+    rng = np.random.default_rng(n * k)
+    q = rng.integers(-8, 8, (n, k))
+    words = O.marlin_encode_int4(O.pack_int4(q))
+    assert words.size == O.marlin_words(n, k, 1)
+    assert np.array_equal(O.marlin_decode_int4(words, n, k), q)
+    c = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    wf = O.marlin_encode_fp8(c)
+    assert wf.size == O.marlin_words(n, k, 2)
+    assert np.array_equal(O.marlin_decode_fp8(wf, n, k), c)
+
+
+# ---------------------------------------------------------------- plm layout
+
+
+def test_plm_layout_int4_known_word():
+    """include/pulsarlm_amd.h: word ((strip*KT + kt)*64 + lane)*4 + t, lane = n%16 + 16*((k%32)/8),
+    even k in nibbles 0-3, odd k in nibbles 4-7, offset binary."""
+    n, k = 32, 256
+    q = np.zeros((n, k), dtype=np.int64)
+    # column 17 (strip 1, col16 = 1), K 128 + 64 + 16 .. +7 -> kt 1, t 2, kq 2.
+    base = 128 + 64 + 16
+    vals = [1, -1, 2, -2, 3, -3, 7, -8]
+    q[17, base:base + 8] = vals
+    words = O.plm_layout_int4(O.pack_int4(q))
+    ktiles = 2
+    lane = 1 + 16 * 2
+    w = int(words[((1 * ktiles + 1) * 64 + lane) * 4 + 2])
+    expect = 0
+    for i, v in enumerate(vals):
+        pos = 4 + i // 2 if i % 2 else i // 2
+        expect |= (v + 8) << (4 * pos)
+    assert w == expect
+    assert int(words[0]) == 0x88888888
+
+
+def test_plm_layout_fp8_known_byte():
+    n, k = 16, 128
+    c = np.zeros((n, k), dtype=np.uint8)
+    c[5, 32 * 3 + 8 * 1 + 6] = 0xAB  # t = 3, kq = 1, i = 6 -> half 1, lane 5 + 16
+    out = O.plm_layout_fp8(c)
+    assert out[1 * 1024 + (5 + 16) * 16 + 8 + 6] == 0xAB
+    assert out.sum() == 0xAB
+
+
+def test_plm_scale_layout():
+    s = np.arange(1, 1 + 4 * 3, dtype=np.float16).reshape(4, 3)  # block_n = 10 -> rows 0..3, K/g = 3
+    out = O.plm_layout_scale(s, 35, 96, 10, 32)
+    assert out.shape == (3, 4, 16)  # strips 3, groups ceil(128/32)=4, per-column
+    assert out[2, 1, 2] == s[34 // 10, 1]
+    assert out[2, 1, 3] == 0  # column 35 is padding
+    assert np.all(out[:, 3, :] == 0)  # padded group
+    out2 = O.plm_layout_scale(np.ones((2, 1), np.float32), 200, 128, 128, 128)
+    assert out2.shape == (13, 1, 1)
+
+
+# ---------------------------------------------------------------- GEMM
+
+
+def test_gemm_ref_matches_torch_fp32():
+    rng = np.random.default_rng(5)
+    x, packed, scale = O.make_w4a16(16, 256, 512, 128, seed=5)
+    w = O.dequant_int4(packed, scale, 1, 128)
+    got = O.gemm_ref(x, w, None)
+    ref = (torch.from_numpy(x) @ torch.from_numpy(w).T).numpy()
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-4)
+    del rng
+
+
+def test_identity_gemm_is_the_dequantized_weight():
+    _, packed, scale = O.make_w4a16(1, 48, 256, 64, seed=6)
+    w = O.dequant_int4(packed, scale, 1, 64)
+    y = O.gemm_ref(np.eye(256, dtype=np.float32), w, "bf16")
+    assert np.array_equal(y, w.T)
+
+
+def test_check_close_flags_a_wrong_sign():
+    x, packed, scale = O.make_w4a16(4, 64, 256, 128, seed=7)
+    w = O.dequant_int4(packed, scale, 1, 128)
+    y = O.gemm_ref(x, w)
+    ok, _ = O.check_close(y, O.gemm_ref(x, w, None))
+    assert ok
+    bad = y.copy()
+    bad[0, 0] = -bad[0, 0] + (1.0 if bad[0, 0] == 0 else 0.0)
+    assert not O.check_close(bad, O.gemm_ref(x, w, None))[0]
+
+
+# ---------------------------------------------------------------- fp8 quantizer
+
+
+def test_fp8_block_quantizer_invariants():
+    rng = np.random.default_rng(8)
+    w = O.bf16_round(rng.standard_normal((300, 256)).astype(np.float32) * 0.02)
+    codes, scale = O.fp8_block_quantize(w, 128, 128)
+    assert scale.shape == (3, 2)
+    deq = O.e4m3_decode(codes) * O.expand_scale(scale, 300, 256, 128, 128)
+    # Each block's largest magnitude maps to 448 exactly.
+    blocks = np.abs(O.e4m3_decode(codes))
+    for r in range(3):
+        for c in range(2):
+            assert blocks[r * 128:(r + 1) * 128, c * 128:(c + 1) * 128].max() == 448.0
+    rel = np.abs(deq - w) / np.maximum(np.abs(w), 1e-30)
+    assert np.all((rel <= 2.0**-4 + 1e-7) | (np.abs(w) < scale.max() * 2**-6))
+    ref = torch.from_numpy(w / O.expand_scale(scale, 300, 256, 128, 128)).to(torch.float8_e4m3fn)
+    assert np.array_equal(codes, ref.view(torch.uint8).numpy())
+
+
+# ---------------------------------------------------------------- MoE
+
+
+def test_routed_experts_matches_per_expert_dense():
+    rng = np.random.default_rng(9)
+    e, h_dim, inter, t, top_k = 8, 64, 32, 40, 2
+    h = O.bf16_round(rng.standard_normal((t, h_dim)).astype(np.float32))
+    gate_up = O.bf16_round(rng.standard_normal((e, 2 * inter, h_dim)).astype(np.float32) * 0.1)
+    down = O.bf16_round(rng.standard_normal((e, h_dim, inter)).astype(np.float32) * 0.1)
+    experts, weights = O.zipf_routing(t, e, top_k, seed=9)
+    a = O.routed_experts_ref(h, experts, weights, gate_up, down)
+    b = O.sparse_moe_ref(h, experts, weights, gate_up, down)
+    assert np.allclose(a, b, rtol=1e-2, atol=1e-2)
+    # The offsets are inclusive cumulative counts and the sort is stable.
+    order, tokens, counts, offsets = O.moe_sort(experts, e)
+    assert offsets[-1] == t * top_k and np.array_equal(np.diff(np.concatenate([[0], offsets])), counts)
+    flat = experts.reshape(-1)[order]
+    assert np.all(np.diff(flat) >= 0)
+    for ex in range(e):
+        idx = order[flat == ex]
+        assert np.all(np.diff(idx) > 0)
+
+
+def test_zipf_routing_is_skewed_and_distinct():
+    experts, w = O.zipf_routing(256, 128, 8, seed=1)
+    assert all(len(set(r)) == 8 for r in experts)
+    counts = np.bincount(experts.reshape(-1), minlength=128)
+    assert counts[0] > 5 * counts[64:].mean()
+    assert np.allclose(w.sum(-1), 1.0, atol=1e-6)
