@@ -121,9 +121,24 @@ int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype,
              void* y, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * W8A8: x is quantized per row (token) to e4m3 on the fly, scale = amax/448,
- * and multiplied with the fp8 weights on the fp8 MFMA. No counterpart in the
- * reference (its fp8 path is W8A16); x and y bf16 or fp16.
+ * Per-row dynamic e4m3 quantization of x [M, K] (bf16/fp16, K % 4 == 0):
+ * x_scale[m] = max(amax(x[m, :]), 1e-12) / 448, codes[m, k] = e4m3_rne(x[m, k] / x_scale[m]).
+ * codes is [M, K] bytes, x_scale fp32 [M]. The rule is the block quantizer of
+ * pulsarlm-core/tests/model/test_qwen3_5.cpp:301-311 applied per row; the
+ * reference has no activation quantizer on its GEMM path.
+ */
+int plm_quantize_rows_e4m3(const void* x, plm_dtype x_dtype, int64_t m, int64_t k,
+                           uint8_t* codes, float* x_scale, void* stream);
+
+/* Workspace bytes plm_gemm_w8a8 needs (quantized x, row scales, split-K). */
+int64_t plm_gemm_w8a8_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
+/*
+ * W8A8: x is quantized per row (token) to e4m3 on the fly (as plm_quantize_rows_e4m3),
+ * and multiplied with e4m3 weights on the fp8 MFMA:
+ * y[m, n] = x_scale[m] * sum_g s[n, g] * sum_{k in g} e4m3(xq[m, k]) * e4m3(w[n, k]).
+ * group_size must be a multiple of 128. No counterpart in the reference (its fp8
+ * path is W8A16, gemm_fp8_marlin_cuda); x and y bf16 or fp16.
  */
 int plm_gemm_w8a8(const void* x, plm_dtype x_dtype,
                   const void* weight, const void* scale, plm_dtype scale_dtype,

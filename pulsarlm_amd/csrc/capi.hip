@@ -2,15 +2,20 @@
 // pulsarlm-core/src/kernels/marlin.cu:538-576) and dispatch between the decode
 // kernel (M <= 16, the reference's small_m switch at marlin.cu:577) and the MFMA
 // kernel.
+#include <algorithm>
+
 #include "plm_common.hpp"
 
 namespace plm {
 int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                   plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
-                  void* y, void* workspace, size_t workspace_bytes, hipStream_t s);
+                  void* y, void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq,
+                  const float* x_scale);
 int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                 plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y,
-                void* workspace, size_t workspace_bytes, hipStream_t s);
+                void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq, const float* x_scale);
+int launch_quantize_rows(const char* op, const void* x, bool bf16, int64_t m, int64_t k, uint8_t* out, float* sx,
+                         bool permuted, hipStream_t s);
 int64_t decode_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k);
 int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k);
 
@@ -62,20 +67,83 @@ int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype, const void* we
     const bool bf16 = x_dtype == PLM_BF16;
     if (m <= kDecodeMaxM)
         return launch_decode(op, format, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y,
-                             workspace, workspace_bytes, as_stream(stream));
+                             workspace, workspace_bytes, as_stream(stream), nullptr, nullptr);
     return launch_mfma(op, format, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, workspace,
-                       workspace_bytes, as_stream(stream));
+                       workspace_bytes, as_stream(stream), nullptr, nullptr);
+}
+
+}  // extern "C"
+
+namespace plm {
+namespace {
+// W8A8 workspace: [split-K region of the GEMM, at least the counters][e4m3 x, M x ktiles x 128][row scales].
+struct w8a8_ws {
+    int64_t gemm, xq, sx, total;
+};
+w8a8_ws w8a8_layout(int64_t m, int64_t n, int64_t k) {
+    w8a8_ws w{};
+    // The split-K counters always keep the front of the workspace, even when this call
+    // does not split, so scratch written here never lands on them.
+    const int64_t gemm = m <= kDecodeMaxM ? decode_workspace_bytes(PLM_FP8, m, n, k) : mfma_workspace_bytes(PLM_FP8, m, n, k);
+    w.gemm = round_up(std::max<int64_t>(gemm, kCounterBytes), 256);
+    w.xq = round_up(m * ceil_div(k, kTileK) * kTileK, 256);
+    w.sx = round_up(m * 4, 256);
+    w.total = w.gemm + w.xq + w.sx;
+    return w;
+}
+}  // namespace
+}  // namespace plm
+
+extern "C" {
+
+int plm_quantize_rows_e4m3(const void* x, plm_dtype x_dtype, int64_t m, int64_t k, uint8_t* codes, float* x_scale,
+                           void* stream) {
+    const char* op = "quantize_rows_e4m3";
+    clear_error();
+    PLM_CHECK_ARG(x_dtype == PLM_BF16 || x_dtype == PLM_FP16, op, "x must be fp16 or bf16");
+    PLM_CHECK_ARG(m >= 0 && k >= 0 && k % 4 == 0 && k <= (int64_t{1} << 30), op, "K must be a multiple of 4");
+    if (m == 0 || k == 0) return PLM_OK;
+    PLM_CHECK_ARG(x && codes && x_scale, op, "null pointer");
+    PLM_CHECK_ARG(aligned(codes, 4), op, "codes must be 4-byte aligned");
+    return launch_quantize_rows(op, x, x_dtype == PLM_BF16, m, k, codes, x_scale, false, as_stream(stream));
+}
+
+int64_t plm_gemm_w8a8_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0) return 0;
+    return w8a8_layout(m, n, k).total;
+}
+
+int plm_gemm_w8a8(const void* x, plm_dtype x_dtype, const void* weight, const void* scale, plm_dtype scale_dtype,
+                  int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+    const char* op = "gemm_fp8_w8a8";
+    clear_error();
+    if (int rc = check_gemm(op, PLM_FP8, x, x_dtype, weight, scale, scale_dtype, m, n, k, block_n, group_size, y))
+        return rc;
+    PLM_CHECK_ARG(group_size % kTileK == 0, op, "group_size must be a multiple of 128 for the fp8 MFMA");
+    if (m == 0 || n == 0) return PLM_OK;
+    const w8a8_ws l = w8a8_layout(m, n, k);
+    if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < l.total) {
+        set_error(op, "workspace of %lld bytes required, %zu given", static_cast<long long>(l.total), workspace_bytes);
+        return PLM_ERR_WORKSPACE;
+    }
+    auto* base = static_cast<uint8_t*>(workspace);
+    auto* xq = base + l.gemm;
+    auto* sx = reinterpret_cast<float*>(base + l.gemm + l.xq);
+    const bool bf16 = x_dtype == PLM_BF16;
+    hipStream_t s = as_stream(stream);
+    if (int rc = launch_quantize_rows(op, x, bf16, m, k, xq, sx, true, s)) return rc;
+    if (m <= kDecodeMaxM)
+        return launch_decode(op, PLM_FP8, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, base,
+                             static_cast<size_t>(l.gemm), s, xq, sx);
+    return launch_mfma(op, PLM_FP8, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, base,
+                       static_cast<size_t>(l.gemm), s, xq, sx);
 }
 
 }  // extern "C"
 
 // Entry points whose kernels are not built yet report so instead of running.
 extern "C" {
-int plm_gemm_w8a8(const void*, plm_dtype, const void*, const void*, plm_dtype, int64_t, int64_t, int64_t, int64_t,
-                  int64_t, void*, void*, size_t, void*) {
-    plm::set_error("gemm_fp8_w8a8", "not implemented");
-    return PLM_ERR_INVALID;
-}
 int plm_grouped_gemm(plm_format, const void*, plm_dtype, const void*, const void*, plm_dtype, const int32_t*, int64_t,
                      int64_t, int64_t, int64_t, int64_t, int64_t, void*, void*, size_t, void*) {
     plm::set_error("grouped_gemm", "not implemented");

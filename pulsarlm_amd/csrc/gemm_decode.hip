@@ -36,20 +36,37 @@ struct decode_args {
     int m, n, k;
     int ktiles, strips, groups, group_size;
     int splits, tiles_per_split;
+    // W8A8 only: e4m3 x in the lane-permuted layout [M][ktiles][128] and per-row scales.
+    const uint8_t* xq;
+    const float* x_scale;
 };
 
-// One wavefront's batch of TPW K tiles for SP strips: weights, raw scales and x.
-template <plm_format F, int SP, int TPW> struct decode_batch {
+// One wavefront's batch of TPW K tiles for SP strips: weights, raw scale bits and x.
+template <plm_format F, int SP, int TPW, bool A8> struct decode_batch {
     u32x4_t w[TPW][SP][fmt_traits<F>::tile_bytes / 1024];
-    float s[TPW][SP];
-    u32x4_t x[TPW][4];
+    uint32_t s[TPW][SP];
+    u32x4_t x[TPW][A8 ? 2 : 4];  // bf16/fp16: 4 steps x 8 values; e4m3: 32 bytes
 };
 
-template <plm_format F, bool BF16, int SP, int TPW, int NW, bool UNIFORM>
+// Loads are raw buffer loads issued unconditionally, so no load sits behind a branch or
+// feeds a select and a whole batch stays in flight (either would make the compiler wait
+// on it at once). Everything that depends only on the wavefront (tile index, K offset,
+// scale group) is computed in scalar registers and passed as the buffer's soffset; the
+// per-lane voffset is fixed for the whole kernel. Out-of-range lanes or tiles (x rows
+// >= M, tiles past the wavefront's range) get offsets past the buffer and read 0 without
+// a memory access; tiles past the range are also skipped by a wave-uniform branch, and
+// strips past N load a clamped strip whose outputs are never stored.
+//
+// A8 (W8A8): x arrives quantized to e4m3 with one fp32 scale per row; each 128-wide
+// K tile is one v_mfma_scale_f32_16x16x128_f8f6f4 per strip on the raw weight bytes,
+// the tile's partial is multiplied by its fp32 block scale, and the row scale is
+// applied before the reduction.
+template <plm_format F, bool BF16, int SP, int TPW, int NW, bool UNIFORM, bool WIDE, bool A8 = false>
 __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
     constexpr int TB = fmt_traits<F>::tile_bytes;
+    constexpr int ES = WIDE ? 4 : 2;  // scale element bytes
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = uniform(threadIdx.x >> 6);
     const int col16 = lane & 15;
     const int kq = lane >> 4;
     const int sg = blockIdx.x;
@@ -60,45 +77,49 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
     const int per_wave = (kt_hi - kt_lo + NW - 1) / NW;
     const int w_lo = kt_lo + wave * per_wave;
     const int w_hi = min(w_lo + per_wave, kt_hi);
-    const bool row_ok = col16 < a.m;
+    const bool bf16_scale = a.scale_dtype == PLM_BF16;
 
-    auto scale_index = [&](int st, int g) -> int64_t {
-        return (static_cast<int64_t>(st < a.strips ? st : a.strips - 1) * a.groups + g) * a.scale_cols +
-               (a.scale_cols == 1 ? 0 : col16);
-    };
+    // Buffers: one weight strip and its scales per j, and x.
+    __amdgpu_buffer_rsrc_t wr[SP], sr[SP];
+#pragma unroll
+    for (int j = 0; j < SP; ++j) {
+        const int stc = min(sg * SP + j, a.strips - 1);
+        wr[j] = make_rsrc(a.w + static_cast<int64_t>(stc) * a.ktiles * TB, static_cast<uint32_t>(a.ktiles) * TB);
+        sr[j] = make_rsrc(static_cast<const uint8_t*>(a.scale) + static_cast<int64_t>(stc) * a.groups * a.scale_cols * ES,
+                          static_cast<uint32_t>(a.groups * a.scale_cols * ES));
+    }
+    const __amdgpu_buffer_rsrc_t xr =
+        A8 ? make_rsrc(a.xq, static_cast<uint32_t>(a.m) * a.ktiles * kTileK)
+           : make_rsrc(a.x, static_cast<uint32_t>(a.m) * a.k * 2);
+    // bf16/fp16: row * K * 2 + 16 kq (+ 64 t + 256 kt); e4m3: row * ktiles * 128 + 32 kq (+ 128 kt).
+    const int x_lane = A8 ? (col16 < a.m ? col16 * a.ktiles * kTileK : kOOB) + 32 * kq
+                          : (col16 < a.m ? col16 * a.k * 2 : kOOB) + 16 * kq;
+    const int w_lane = lane * 16;
+    const int s_lane = (a.scale_cols == 1 ? 0 : col16) * ES;
 
-    auto load_batch = [&](decode_batch<F, SP, TPW>& b, int kt0) {
+    auto load_batch = [&](decode_batch<F, SP, TPW, A8>& b, int kt0) {
 #pragma unroll
         for (int tt = 0; tt < TPW; ++tt) {
             const int kt = kt0 + tt;
-            const bool kt_ok = kt < w_hi;
+            const bool ok = kt < w_hi;  // wave-uniform
+            const int w_off = ok ? kt * TB : kOOB;
+            const int x_off = ok ? kt * kTileK * (A8 ? 1 : 2) : kOOB;
 #pragma unroll
             for (int j = 0; j < SP; ++j) {
-                const int st = sg * SP + j;
 #pragma unroll
-                for (int h = 0; h < TB / 1024; ++h) {
-                    if (kt_ok && st < a.strips) {
-                        const int64_t off =
-                            ((static_cast<int64_t>(st) * a.ktiles + kt) * (TB / 1024) + h) * 1024 + lane * 16;
-                        b.w[tt][j][h] = *reinterpret_cast<const u32x4_t*>(a.w + off);
-                    } else {
-                        b.w[tt][j][h] = (F == PLM_INT4)
-                                            ? u32x4_t{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u}
-                                            : u32x4_t{0u, 0u, 0u, 0u};
-                    }
+                for (int h = 0; h < TB / 1024; ++h) b.w[tt][j][h] = buffer_load16(wr[j], w_lane + h * 1024, w_off);
+                if constexpr (UNIFORM) {
+                    const int s_off = ok ? (kt * kTileK / a.group_size) * a.scale_cols * ES : kOOB;
+                    if constexpr (WIDE) b.s[tt][j] = buffer_load_u32(sr[j], s_lane, s_off);
+                    else b.s[tt][j] = buffer_load_u16(sr[j], s_lane, s_off);
                 }
-                if constexpr (UNIFORM)
-                    b.s[tt][j] = kt_ok ? load_scale(a.scale, scale_index(st, kt * kTileK / a.group_size),
-                                                    a.scale_dtype)
-                                       : 0.f;
             }
+            if constexpr (A8) {
+                b.x[tt][0] = buffer_load16(xr, x_lane, x_off);
+                b.x[tt][1] = buffer_load16(xr, x_lane + 16, x_off);
+            } else {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int k0 = kt * kTileK + 32 * t + 8 * kq;
-                if (kt_ok && row_ok && k0 < a.k)
-                    b.x[tt][t] = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<int64_t>(col16) * a.k + k0);
-                else
-                    b.x[tt][t] = u32x4_t{0u, 0u, 0u, 0u};
+                for (int t = 0; t < 4; ++t) b.x[tt][t] = buffer_load16(xr, x_lane + 64 * t, x_off);
             }
         }
     };
@@ -107,26 +128,48 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
 #pragma unroll
     for (int j = 0; j < SP; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    auto compute_batch = [&](const decode_batch<F, SP, TPW>& b, int kt0) {
+    auto compute_batch = [&](const decode_batch<F, SP, TPW, A8>& b, int kt0) {
 #pragma unroll
         for (int tt = 0; tt < TPW; ++tt) {
             const int kt = kt0 + tt;
-            if (kt >= w_hi) break;
+            if (kt >= w_hi) break;  // wave-uniform
+            if constexpr (A8) {  // x past K is already zero in the quantized copy
+#pragma unroll
+                for (int j = 0; j < SP; ++j) {
+                    const float s = scale_from_bits<WIDE>(b.s[tt][j], bf16_scale);
+                    const i32x8_t av = __builtin_bit_cast(i32x8_t, u32x8_cat(b.x[tt][0], b.x[tt][1]));
+                    const i32x8_t bv = __builtin_bit_cast(i32x8_t, u32x8_cat(b.w[tt][j][0], b.w[tt][j][TB / 1024 - 1]));
+                    const f32x4_t part = mfma16x16x128_fp8(av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[j][i] = __builtin_fmaf(s, part[i], acc[j][i]);
+                }
+                continue;
+            }
+            u32x4_t xs[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xs[t] = b.x[tt][t];
+            if ((kt + 1) * kTileK > a.k) {  // wave-uniform: partial last tile, zero x past K
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    if (kt * kTileK + 32 * t + 8 * kq >= a.k) xs[t] = u32x4_t{0u, 0u, 0u, 0u};
+            }
 #pragma unroll
             for (int j = 0; j < SP; ++j) {
-                const int st = sg * SP + j;
                 float s_tile = 0.f;
                 int4_scale k4{};
                 if constexpr (UNIFORM) {
-                    s_tile = round_to<BF16>(b.s[tt][j]);
-                    if constexpr (F == PLM_INT4) k4 = make_int4_scale<BF16>(b.s[tt][j]);
+                    const float raw = scale_from_bits<WIDE>(b.s[tt][j], bf16_scale);
+                    s_tile = round_to<BF16>(raw);
+                    if constexpr (F == PLM_INT4) k4 = make_int4_scale<BF16>(raw);
                 }
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     float s = s_tile;
                     if constexpr (!UNIFORM) {
                         const int g = (kt * kTileK + 32 * t + 8 * kq) / a.group_size;
-                        const float raw = load_scale(a.scale, scale_index(st, g), a.scale_dtype);
+                        const uint32_t bits = WIDE ? buffer_load_u32(sr[j], s_lane + g * a.scale_cols * ES, 0)
+                                                   : buffer_load_u16(sr[j], s_lane + g * a.scale_cols * ES, 0);
+                        const float raw = scale_from_bits<WIDE>(bits, bf16_scale);
                         s = round_to<BF16>(raw);
                         if constexpr (F == PLM_INT4) k4 = make_int4_scale<BF16>(raw);
                     }
@@ -137,24 +180,26 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
                         const u32x4_t& v = b.w[tt][j][t >> 1];
                         bop = dq_fp8<BF16>(v[(t & 1) * 2], v[(t & 1) * 2 + 1], s);
                     }
-                    acc[j] = mfma16x16x32<BF16>(b.x[tt][t], bop, acc[j]);
+                    acc[j] = mfma16x16x32<BF16>(xs[t], bop, acc[j]);
                 }
             }
         }
     };
 
-    // Register double buffering: batch i+1's loads are in flight while batch i computes.
-    decode_batch<F, SP, TPW> b0, b1;
-    int kt = w_lo;
-    if (kt < w_hi) load_batch(b0, kt);
-    while (kt < w_hi) {
-        if (kt + TPW < w_hi) load_batch(b1, kt + TPW);
-        compute_batch(b0, kt);
-        kt += TPW;
-        if (kt >= w_hi) break;
-        if (kt + TPW < w_hi) load_batch(b0, kt + TPW);
-        compute_batch(b1, kt);
-        kt += TPW;
+    // One batch in flight per wavefront; latency is hidden by the other resident
+    // wavefronts (a register double buffer gets rotated into copies that wait).
+    decode_batch<F, SP, TPW, A8> b;
+    for (int kt = w_lo; kt < w_hi; kt += TPW) {
+        load_batch(b, kt);
+        compute_batch(b, kt);
+    }
+    if constexpr (A8) {  // row scales; rows past M are never stored
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float sx = a.x_scale[min(4 * kq + i, a.m - 1)];
+#pragma unroll
+            for (int j = 0; j < SP; ++j) acc[j][i] *= sx;
+        }
     }
 
     // Cross-wavefront reduction in a fixed order.
@@ -229,12 +274,20 @@ decode_config choose_decode(plm_format f, int64_t m, int64_t n, int64_t k) {
     decode_config c{};
     const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
     const int64_t cus = cu_count();
-    c.sp = (m > 4 && strips >= 2 * cus) ? 2 : 1;
-    c.nw = ktiles >= 32 ? 16 : (ktiles >= 8 ? 8 : 4);
-    c.tpw = 2;
+    // Measured on MI355X at the Qwen3-8B shapes (int4, g128): two strips per wavefront
+    // (halving the x traffic per weight byte) pays when there are many strips or M > 4;
+    // otherwise one strip and two K tiles per batch; 16 wavefronts split K.
+    if (strips >= 4 * cus) {
+        c.sp = 2, c.tpw = 1, c.nw = 16;
+    } else if (m > 4) {
+        c.sp = 2, c.tpw = 1, c.nw = 8;
+    } else {
+        c.sp = 1, c.tpw = 2, c.nw = 16;
+    }
+    if (ktiles < 2 * c.nw) c.nw = ktiles >= 16 ? 8 : 4;
     if (const char* env = getenv("PLM_DECODE")) {  // "sp,tpw,nw" for tuning sweeps
         int sp = 0, t = 0, nw = 0;
-        if (sscanf(env, "%d,%d,%d", &sp, &t, &nw) == 3 && (sp == 1 || sp == 2) && (t == 1 || t == 2 || t == 4) &&
+        if (sscanf(env, "%d,%d,%d", &sp, &t, &nw) == 3 && (sp == 1 || sp == 2) && (t == 1 || t == 2) &&
             (nw == 4 || nw == 8 || nw == 16)) {
             c.sp = sp;
             c.tpw = t;
@@ -262,10 +315,21 @@ namespace {
 template <plm_format F, bool BF16, int SP, int TPW, int NW>
 void launch_decode_t(const decode_args& a, int strip_groups, bool uniform, hipStream_t s) {
     dim3 grid(strip_groups, a.splits);
-    if (uniform)
-        decode_kernel<F, BF16, SP, TPW, NW, true><<<grid, NW * 64, 0, s>>>(a);
-    else
-        decode_kernel<F, BF16, SP, TPW, NW, false><<<grid, NW * 64, 0, s>>>(a);
+    const bool wide = a.scale_dtype == PLM_FP32;
+    if constexpr (F == PLM_FP8) {
+        if (a.xq != nullptr) {  // W8A8 (group_size % 128 == 0 is checked by the caller)
+            if (wide) decode_kernel<F, BF16, SP, TPW, NW, true, true, true><<<grid, NW * 64, 0, s>>>(a);
+            else decode_kernel<F, BF16, SP, TPW, NW, true, false, true><<<grid, NW * 64, 0, s>>>(a);
+            return;
+        }
+    }
+    if (uniform) {
+        if (wide) decode_kernel<F, BF16, SP, TPW, NW, true, true><<<grid, NW * 64, 0, s>>>(a);
+        else decode_kernel<F, BF16, SP, TPW, NW, true, false><<<grid, NW * 64, 0, s>>>(a);
+    } else {
+        if (wide) decode_kernel<F, BF16, SP, TPW, NW, false, true><<<grid, NW * 64, 0, s>>>(a);
+        else decode_kernel<F, BF16, SP, TPW, NW, false, false><<<grid, NW * 64, 0, s>>>(a);
+    }
 }
 
 template <plm_format F, bool BF16, int SP, int TPW>
@@ -279,11 +343,8 @@ void launch_decode_nw(const decode_args& a, const decode_config& c, bool uniform
 
 template <plm_format F, bool BF16, int SP>
 void launch_decode_sp(const decode_args& a, const decode_config& c, bool uniform, hipStream_t s) {
-    switch (c.tpw) {
-        case 1: launch_decode_nw<F, BF16, SP, 1>(a, c, uniform, s); break;
-        case 4: launch_decode_nw<F, BF16, SP, 4>(a, c, uniform, s); break;
-        default: launch_decode_nw<F, BF16, SP, 2>(a, c, uniform, s); break;
-    }
+    if (c.tpw == 1) launch_decode_nw<F, BF16, SP, 1>(a, c, uniform, s);
+    else launch_decode_nw<F, BF16, SP, 2>(a, c, uniform, s);
 }
 
 template <plm_format F, bool BF16>
@@ -295,7 +356,8 @@ void launch_decode_f(const decode_args& a, const decode_config& c, bool uniform,
 
 int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                   plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
-                  void* y, void* workspace, size_t workspace_bytes, hipStream_t s) {
+                  void* y, void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq,
+                  const float* x_scale) {
     const decode_config c = choose_decode(f, m, n, k);
     const layout_dims d = make_dims(n, k, block_n, group_size);
     decode_args a{};
@@ -314,7 +376,11 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
     a.group_size = static_cast<int>(group_size);
     a.splits = c.splits;
     a.tiles_per_split = c.tiles_per_split;
+    a.xq = xq;
+    a.x_scale = x_scale;
     PLM_CHECK_ARG(c.splits > 0, op, "N = %lld is too large for the decode kernel", static_cast<long long>(n));
+    // Buffer offsets stay below kOOB: x is at most 16 x K bf16, a weight strip K/128 tiles.
+    PLM_CHECK_ARG(k <= (int64_t{1} << 24), op, "K must be at most 2^24");
     if (c.splits > 1) {
         const int64_t need = decode_workspace_bytes(f, m, n, k);
         if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need) {

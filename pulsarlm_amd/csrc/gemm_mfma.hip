@@ -1,33 +1,36 @@
-// MFMA dequant-GEMM for M > 16 (prefill): y[M, N] = x[M, K] @ dequant(W)^T.
+// MFMA dequant-GEMM for M > 16 (prefill), its W8A8 form and its grouped (MoE) form:
+// y[M, N] = x[M, K] @ dequant(W)^T.
 //
 // Counterpart of the reference's marlin_kernel at tile_m = 64 (pulsarlm-core/src/kernels/
-// marlin.cu:251-389; dispatch :577-596) and its split-K combine
-// (pulsarlm-core/inc/pulsarlm/kernels/dequant_gemm_common.cuh:99-133).
+// marlin.cu:251-389; dispatch :577-596) with its split-K combine
+// (pulsarlm-core/inc/pulsarlm/kernels/dequant_gemm_common.cuh:99-133), and, in grouped
+// mode, of one at::_grouped_mm of routed_experts (pulsarlm-core/src/engine/model/
+// paged_forward.cpp:124-125).
 //
 // gfx950 design:
-// * Workgroup tile BM x 128 columns x 128-wide K steps; four wavefronts in a 2 x 2
-//   grid, each owning (BM/2) x 64 outputs as 16 x 16 tiles of v_mfma_f32_16x16x32.
-// * The x tile (bf16/fp16) and the packed weight tiles (1 KiB int4 / 2 KiB fp8 per
-//   16-column strip, copied verbatim from the plm layout) are staged through LDS,
-//   double buffered, with the next K step's global loads in flight during the
-//   current step's MFMAs.
-// * Each wavefront dequantizes its strips in registers to round(q * round(s)),
-//   bit-identical to the reference's fragment values (marlin.cu:123-151,180-194),
-//   with the shared dq_int4 / dq_fp8 sequences.
-// * Split-K across workgroups when the output has too few tiles to fill the GPU,
-//   reduced deterministically by the last workgroup to arrive.
+// * Workgroup tile (WM*MT*16) x (WN*NS*16) over 128-wide K steps; WM x WN wavefronts,
+//   each owning MT x NS tiles of v_mfma_f32_16x16x32 (bf16/fp16) -- 128 x 64 per
+//   wavefront in the large configuration (256 x 128 per workgroup, one wavefront per
+//   SIMD with the full 512 registers), so each dequantized weight feeds 8 MFMAs and the
+//   dequant VALU work is about half the MFMA time, interleaved with it.
+// * The x tile and the packed weight tiles (1 KiB int4 / 2 KiB fp8 per 16-column strip,
+//   copied verbatim from the plm layout) are staged through LDS; the next K step's global
+//   loads are in flight in registers during the current step's MFMAs.
+// * Weights are dequantized in registers to round(q * round(s)), bit-identical to the
+//   reference's fragment values (shared dq_int4 / dq_fp8).
+// * A8 (W8A8): x is e4m3 (quantized per row beforehand) and every 128-wide K tile is one
+//   v_mfma_scale_f32_16x16x128_f8f6f4 per output tile on the raw weight bytes; the tile's
+//   partial is scaled by the weight block scale and, at the end, by the row scale.
+// * Grouped: each work tile is (expert, block of that expert's rows); rows may be gathered
+//   through a row index (the tokens routed to the expert) and the expert's weights and
+//   scales are found at a fixed stride.
+// * Split-K across workgroups when the output has too few tiles to fill the GPU, reduced
+//   deterministically by the last workgroup to arrive.
 #include <type_traits>
 
 #include "plm_common.hpp"
 
 namespace plm {
-
-namespace {
-
-constexpr int kWaves = 4;
-constexpr int kBN = 128;                  // 8 strips
-constexpr int kStrips = kBN / kTileN;     // 8
-constexpr int kARowBytes = kTileK * 2 + 16;  // padded LDS row: 128 halves + 16 B
 
 struct mfma_args {
     const uint16_t* x;
@@ -40,149 +43,235 @@ struct mfma_args {
     int m, n, k;
     int ktiles, strips, groups, group_size;
     int splits, tiles_per_split;
-    int m_blocks;
+    int m_blocks, n_blocks;
+    // A8
+    const uint8_t* xq;      // e4m3 [M][ktiles][128], lane-permuted within each tile
+    const float* x_scale;   // [M]
+    // Grouped
+    const int32_t* tiles;      // [max_tiles][3]: expert, first row, rows (rows == 0: idle)
+    const int32_t* row_index;  // gather: A row r is x[row_index[r]] (null: x[r])
+    int64_t w_expert_bytes;
+    int64_t s_expert_bytes;
 };
 
-template <plm_format F, bool BF16, int BM, bool UNIFORM>
-__global__ void __launch_bounds__(kWaves * 64) mfma_kernel(mfma_args a) {
-    constexpr int TB = fmt_traits<F>::tile_bytes;
-    constexpr int MT = BM / 2 / 16;  // m tiles per wavefront
-    constexpr int A_BYTES = BM * kARowBytes;
-    constexpr int B_BYTES = kStrips * TB;
-    constexpr int A_LOADS = BM * kTileK * 2 / 16 / (kWaves * 64);  // 16-byte loads per thread
-    constexpr int B_LOADS = B_BYTES / 16 / (kWaves * 64);
-    static_assert(A_LOADS * 16 * kWaves * 64 == BM * kTileK * 2, "A tile split");
-    static_assert(B_LOADS * 16 * kWaves * 64 == B_BYTES, "B tile split");
+namespace {
 
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][A_BYTES + B_BYTES];
+template <bool A8> struct a_traits {
+    static constexpr int row_bytes = A8 ? kTileK : kTileK * 2;
+    static constexpr int lds_row = row_bytes + 16;  // padded LDS row
+};
+
+template <plm_format F, bool BF16, bool UNIFORM, bool A8, bool GROUPED, int WM, int WN, int MT, int NS>
+__global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
+    constexpr int NT = WM * WN * 64;  // threads
+    constexpr int TB = fmt_traits<F>::tile_bytes;
+    constexpr int BM = WM * MT * 16;
+    constexpr int BS = WN * NS;  // strips per workgroup
+    constexpr int ARB = a_traits<A8>::row_bytes;
+    constexpr int ALR = a_traits<A8>::lds_row;
+    constexpr int A_BYTES = BM * ALR;
+    constexpr int B_BYTES = BS * TB;
+    constexpr int A_CHUNKS = BM * ARB / 16;
+    constexpr int B_CHUNKS = B_BYTES / 16;
+    constexpr int A_LOADS = (A_CHUNKS + NT - 1) / NT;
+    constexpr int B_LOADS = (B_CHUNKS + NT - 1) / NT;
+    constexpr int CPR = ARB / 16;  // 16-byte chunks per A row
+
+    __shared__ __attribute__((aligned(16))) uint8_t lds[A_BYTES + B_BYTES];
     __shared__ uint32_t last_flag;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int lane = tid & 63;
+    const int wave = uniform(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
     const int col16 = lane & 15, kq = lane >> 4;
-    const int mb = blockIdx.x % a.m_blocks;
-    const int nb = blockIdx.x / a.m_blocks;
     const int split = blockIdx.y;
-    const int m0 = mb * BM;
-    const int strip0 = nb * kStrips;
+
+    // Work tile: (row block, column block), grouped: (expert tile, column block).
+    int nb, expert = 0, row0, rows;
+    if constexpr (GROUPED) {
+        const int tile = blockIdx.x / a.n_blocks;
+        nb = blockIdx.x % a.n_blocks;
+        expert = a.tiles[3 * tile];
+        row0 = a.tiles[3 * tile + 1];
+        rows = a.tiles[3 * tile + 2];
+        if (rows <= 0) return;  // uniform across the workgroup
+    } else {
+        const int mb = blockIdx.x % a.m_blocks;
+        nb = blockIdx.x / a.m_blocks;
+        row0 = mb * BM;
+        rows = min(BM, a.m - row0);
+    }
+    const int strip0 = nb * BS;
     const int kt_begin = split * a.tiles_per_split;
     const int kt_end = min(kt_begin + a.tiles_per_split, a.ktiles);
+    const uint8_t* wbase = a.w + (GROUPED ? expert * a.w_expert_bytes : 0);
+    const void* sbase = static_cast<const uint8_t*>(a.scale) + (GROUPED ? expert * a.s_expert_bytes : 0);
 
-    f32x4_t acc[MT][4];
+    f32x4_t acc[MT][NS];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NS; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // Source row of A chunk c: row0 + c / CPR, gathered through row_index for grouped
+    // calls (those are kept in registers; plain calls recompute them).
+    int a_src[GROUPED ? A_LOADS : 1];
+    auto src_row = [&](int i) -> int {
+        const int c = tid + i * NT;
+        const int r = c / CPR;
+        if (c >= A_CHUNKS || r >= rows) return -1;
+        if constexpr (GROUPED) return a.row_index != nullptr ? a.row_index[row0 + r] : row0 + r;
+        return row0 + r;
+    };
+    if constexpr (GROUPED) {
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i) a_src[i] = src_row(i);
+    }
 
     u32x4_t ra[A_LOADS], rb[B_LOADS];
     auto global_load = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
-            const int c = tid + i * kWaves * 64;  // 16-byte chunk id: row c/16, K chunk c%16
-            const int row = m0 + c / 16;
-            const int kk = kt * kTileK + (c % 16) * 8;
-            if (row < a.m && kk < a.k)
-                ra[i] = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<int64_t>(row) * a.k + kk);
-            else
-                ra[i] = u32x4_t{0u, 0u, 0u, 0u};
+            const int c = tid + i * NT;
+            const int cc = c % CPR;
+            u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+            const int src = GROUPED ? a_src[GROUPED ? i : 0] : src_row(i);
+            if (src >= 0) {
+                if constexpr (A8) {
+                    v = *reinterpret_cast<const u32x4_t*>(a.xq + (static_cast<int64_t>(src) * a.ktiles + kt) * kTileK +
+                                                          cc * 16);
+                } else {
+                    const int kk = kt * kTileK + cc * 8;
+                    if (kk < a.k) v = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<int64_t>(src) * a.k + kk);
+                }
+            }
+            ra[i] = v;
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; ++i) {
-            const int c = tid + i * kWaves * 64;  // chunk within the 8-strip tile group
+            const int c = tid + i * NT;
             const int s = c / (TB / 16);
-            const int within = c % (TB / 16);
             const int st = strip0 + s;
-            if (st < a.strips)
-                rb[i] = *reinterpret_cast<const u32x4_t*>(a.w + (static_cast<int64_t>(st) * a.ktiles + kt) * TB +
-                                                          within * 16);
+            if (c < B_CHUNKS && st < a.strips)
+                rb[i] = *reinterpret_cast<const u32x4_t*>(wbase + (static_cast<int64_t>(st) * a.ktiles + kt) * TB +
+                                                          (c % (TB / 16)) * 16);
             else
                 rb[i] = (F == PLM_INT4) ? u32x4_t{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u}
                                         : u32x4_t{0u, 0u, 0u, 0u};
         }
     };
-    auto lds_store = [&](int buf) {
+    auto lds_store = [&]() {
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) {
-            const int c = tid + i * kWaves * 64;
-            *reinterpret_cast<u32x4_t*>(&lds[buf][(c / 16) * kARowBytes + (c % 16) * 16]) = ra[i];
+            const int c = tid + i * NT;
+            if (c < A_CHUNKS) *reinterpret_cast<u32x4_t*>(&lds[(c / CPR) * ALR + (c % CPR) * 16]) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < B_LOADS; ++i) {
-            const int c = tid + i * kWaves * 64;
-            *reinterpret_cast<u32x4_t*>(&lds[buf][A_BYTES + c * 16]) = rb[i];
+            const int c = tid + i * NT;
+            if (c < B_CHUNKS) *reinterpret_cast<u32x4_t*>(&lds[A_BYTES + c * 16]) = rb[i];
         }
+    };
+
+    auto scale_raw = [&](int j, int kt, int t) -> float {
+        const int g = UNIFORM ? kt * kTileK / a.group_size : (kt * kTileK + 32 * t + 8 * kq) / a.group_size;
+        const int st = min(strip0 + wn * NS + j, a.strips - 1);
+        const int64_t sidx = (static_cast<int64_t>(st) * a.groups + g) * a.scale_cols + (a.scale_cols == 1 ? 0 : col16);
+        return load_scale(sbase, sidx, a.scale_dtype);
     };
 
     if (kt_begin < kt_end) {
         global_load(kt_begin);
-        lds_store(0);
+        lds_store();
     }
     __syncthreads();
 
     for (int kt = kt_begin; kt < kt_end; ++kt) {
-        const int buf = (kt - kt_begin) & 1;
         if (kt + 1 < kt_end) global_load(kt + 1);
 
-        // Scales of this wavefront's 4 strips (one per tile when the group spans it).
-        auto scale_raw = [&](int j, int t) -> float {
-            const int g = (kt * kTileK + 32 * t + 8 * kq) / a.group_size;
-            const int st = min(strip0 + wn * 4 + j, a.strips - 1);
-            const int64_t sidx =
-                (static_cast<int64_t>(st) * a.groups + g) * a.scale_cols + (a.scale_cols == 1 ? 0 : col16);
-            return load_scale(a.scale, sidx, a.scale_dtype);
-        };
-        float sr[4];
+        float sr[NS];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sr[j] = UNIFORM ? scale_raw(j, 0) : 0.f;
-        const uint8_t* la = &lds[buf][0];
-        const uint8_t* lb = &lds[buf][A_BYTES];
-        u32x4_t wv[4][TB / 1024];
+        for (int j = 0; j < NS; ++j) sr[j] = UNIFORM ? scale_raw(j, kt, 0) : 0.f;
+        u32x4_t wv[NS][TB / 1024];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NS; ++j)
 #pragma unroll
             for (int h = 0; h < TB / 1024; ++h)
-                wv[j][h] = *reinterpret_cast<const u32x4_t*>(lb + (wn * 4 + j) * TB + h * 1024 + lane * 16);
+                wv[j][h] = *reinterpret_cast<const u32x4_t*>(&lds[A_BYTES + (wn * NS + j) * TB + h * 1024 + lane * 16]);
 
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            u32x4_t af[MT];
+        if constexpr (A8) {
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
-                const int row = wm * (BM / 2) + i * 16 + col16;
-                af[i] = *reinterpret_cast<const u32x4_t*>(la + row * kARowBytes + (32 * t + 8 * kq) * 2);
-            }
+                const int row = wm * MT * 16 + i * 16 + col16;
+                const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(&lds[row * ALR + kq * 32]);
+                const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(&lds[row * ALR + kq * 32 + 16]);
+                const i32x8_t av = __builtin_bit_cast(i32x8_t, u32x8_cat(a0, a1));
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float raw = UNIFORM ? sr[j] : scale_raw(j, t);
-                u32x4_t b;
-                if constexpr (F == PLM_INT4) {
-                    b = dq_int4<BF16>(wv[j][0][t], make_int4_scale<BF16>(raw));
-                } else {
-                    b = dq_fp8<BF16>(wv[j][t >> 1][(t & 1) * 2], wv[j][t >> 1][(t & 1) * 2 + 1], round_to<BF16>(raw));
+                for (int j = 0; j < NS; ++j) {
+                    const i32x8_t bv = __builtin_bit_cast(i32x8_t, u32x8_cat(wv[j][0], wv[j][TB / 1024 - 1]));
+                    const f32x4_t part = mfma16x16x128_fp8(av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sr[j], part[r], acc[i][j][r]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                u32x4_t af[MT];
+#pragma unroll
+                for (int i = 0; i < MT; ++i) {
+                    const int row = wm * MT * 16 + i * 16 + col16;
+                    af[i] = *reinterpret_cast<const u32x4_t*>(&lds[row * ALR + (32 * t + 8 * kq) * 2]);
                 }
 #pragma unroll
-                for (int i = 0; i < MT; ++i) acc[i][j] = mfma16x16x32<BF16>(af[i], b, acc[i][j]);
+                for (int j = 0; j < NS; ++j) {
+                    const float raw = UNIFORM ? sr[j] : scale_raw(j, kt, t);
+                    u32x4_t b;
+                    if constexpr (F == PLM_INT4) {
+                        b = dq_int4<BF16>(wv[j][0][t], make_int4_scale<BF16>(raw));
+                    } else {
+                        b = dq_fp8<BF16>(wv[j][t >> 1][(t & 1) * 2], wv[j][t >> 1][(t & 1) * 2 + 1],
+                                         round_to<BF16>(raw));
+                    }
+#pragma unroll
+                    for (int i = 0; i < MT; ++i) acc[i][j] = mfma16x16x32<BF16>(af[i], b, acc[i][j]);
+                }
             }
         }
         __syncthreads();
-        if (kt + 1 < kt_end) lds_store(buf ^ 1);
-        __syncthreads();
+        if (kt + 1 < kt_end) {
+            lds_store();
+            __syncthreads();
+        }
     }
 
-    // Epilogue: lane holds column col16 of strip (strip0 + wn*4 + j), rows 4*kq + r of m tile i.
+    if constexpr (A8) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = row0 + wm * MT * 16 + i * 16 + 4 * kq + r;
+                const float sx = a.x_scale[min(row, a.m - 1)];
+#pragma unroll
+                for (int j = 0; j < NS; ++j) acc[i][j][r] *= sx;
+            }
+    }
+
+    // Epilogue: lane holds column col16 of strip (strip0 + wn*NS + j), rows 4*kq + r of m tile i.
     const int64_t mn = static_cast<int64_t>(a.m) * a.n;
     if (a.splits == 1) {
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int col = (strip0 + wn * 4 + j) * kTileN + col16;
+            for (int j = 0; j < NS; ++j) {
+                const int col = (strip0 + wn * NS + j) * kTileN + col16;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int row = m0 + wm * (BM / 2) + i * 16 + 4 * kq + r;
-                    if (row < a.m && col < a.n)
-                        a.y[static_cast<int64_t>(row) * a.n + col] = static_cast<uint16_t>(to_bits16<BF16>(acc[i][j][r]));
+                    const int lr = wm * MT * 16 + i * 16 + 4 * kq + r;
+                    if (lr < rows && col < a.n)
+                        a.y[static_cast<int64_t>(row0 + lr) * a.n + col] =
+                            static_cast<uint16_t>(to_bits16<BF16>(acc[i][j][r]));
                 }
             }
         return;
@@ -190,22 +279,22 @@ __global__ void __launch_bounds__(kWaves * 64) mfma_kernel(mfma_args a) {
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int col = (strip0 + wn * 4 + j) * kTileN + col16;
+        for (int j = 0; j < NS; ++j) {
+            const int col = (strip0 + wn * NS + j) * kTileN + col16;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = m0 + wm * (BM / 2) + i * 16 + 4 * kq + r;
-                if (row < a.m && col < a.n)
-                    store_partial(&a.partial[split * mn + static_cast<int64_t>(row) * a.n + col], acc[i][j][r]);
+                const int lr = wm * MT * 16 + i * 16 + 4 * kq + r;
+                if (lr < rows && col < a.n)
+                    store_partial(&a.partial[split * mn + static_cast<int64_t>(row0 + lr) * a.n + col], acc[i][j][r]);
             }
         }
     if (!arrive_last(&a.counters[blockIdx.x], static_cast<uint32_t>(a.splits), &last_flag)) return;
-    // Sum this tile's partials in split order; threads sweep the BM x 128 tile row-major.
-    for (int e = tid; e < BM * kBN; e += kWaves * 64) {
-        const int row = m0 + e / kBN;
-        const int col = strip0 * kTileN + e % kBN;
-        if (row < a.m && col < a.n) {
-            const int64_t off = static_cast<int64_t>(row) * a.n + col;
+    // Sum this tile's partials in split order; threads sweep the tile row-major.
+    for (int e = tid; e < BM * BS * kTileN; e += NT) {
+        const int lr = e / (BS * kTileN);
+        const int col = strip0 * kTileN + e % (BS * kTileN);
+        if (lr < rows && col < a.n) {
+            const int64_t off = static_cast<int64_t>(row0 + lr) * a.n + col;
             float s = 0.f;
             for (int sp = 0; sp < a.splits; ++sp) s += load_partial(&a.partial[sp * mn + off]);
             a.y[off] = static_cast<uint16_t>(to_bits16<BF16>(s));
@@ -213,20 +302,34 @@ __global__ void __launch_bounds__(kWaves * 64) mfma_kernel(mfma_args a) {
     }
 }
 
+// Tile shapes: {WM, WN, MT, NS}.
+struct shape {
+    int wm, wn, mt, ns;
+    constexpr int bm() const { return wm * mt * 16; }
+    constexpr int bs() const { return wn * ns; }
+};
+constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts (one per SIMD, 512 registers)
+constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
+
+}  // namespace
+
 struct mfma_config {
-    int bm;
+    bool large;
     int m_blocks, n_blocks;
     int splits, tiles_per_split;
 };
 
 mfma_config choose_mfma(int64_t m, int64_t n, int64_t k) {
     mfma_config c{};
-    c.bm = 128;
-    c.m_blocks = static_cast<int>(ceil_div(m, c.bm));
-    c.n_blocks = static_cast<int>(ceil_div(n, kBN));
-    const int64_t ktiles = ceil_div(k, kTileK);
-    const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
     const int64_t cus = cu_count();
+    const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
+    const int64_t large_tiles = ceil_div(m, kLarge.bm()) * ceil_div(strips, kLarge.bs());
+    c.large = large_tiles >= cus;
+    if (const char* env = getenv("PLM_MFMA")) c.large = env[0] == 'L';  // tuning sweeps
+    const shape sh = c.large ? kLarge : kSmall;
+    c.m_blocks = static_cast<int>(ceil_div(m, sh.bm()));
+    c.n_blocks = static_cast<int>(ceil_div(strips, sh.bs()));
+    const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
     int64_t splits = 1;
     if (tiles < cus && tiles <= kMaxCounters) splits = std::min<int64_t>(ceil_div(cus, tiles), ktiles);
     c.tiles_per_split = static_cast<int>(ceil_div(ktiles, splits));
@@ -234,20 +337,50 @@ mfma_config choose_mfma(int64_t m, int64_t n, int64_t k) {
     return c;
 }
 
-}  // namespace
-
 int64_t mfma_workspace_bytes(plm_format, int64_t m, int64_t n, int64_t k) {
     const mfma_config c = choose_mfma(m, n, k);
     if (c.splits <= 1) return 0;
     return kCounterBytes + static_cast<int64_t>(c.splits) * m * n * 4;
 }
 
-int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
-                plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y,
-                void* workspace, size_t workspace_bytes, hipStream_t s) {
-    const mfma_config c = choose_mfma(m, n, k);
+namespace {
+template <plm_format F, bool BF16, bool UNIFORM, bool A8, bool GROUPED>
+void launch_shape(const mfma_args& a, bool large, dim3 grid, hipStream_t s) {
+    if (large)
+        mfma_kernel<F, BF16, UNIFORM, A8, GROUPED, kLarge.wm, kLarge.wn, kLarge.mt, kLarge.ns>
+            <<<grid, kLarge.wm * kLarge.wn * 64, 0, s>>>(a);
+    else
+        mfma_kernel<F, BF16, UNIFORM, A8, GROUPED, kSmall.wm, kSmall.wn, kSmall.mt, kSmall.ns>
+            <<<grid, kSmall.wm * kSmall.wn * 64, 0, s>>>(a);
+}
+
+template <plm_format F, bool BF16, bool GROUPED>
+void launch_mode(const mfma_args& a, bool large, bool uniform, bool a8, dim3 grid, hipStream_t s) {
+    if constexpr (F == PLM_FP8 && !GROUPED) {
+        if (a8) {
+            launch_shape<F, BF16, true, true, GROUPED>(a, large, grid, s);
+            return;
+        }
+    }
+    if (uniform) launch_shape<F, BF16, true, false, GROUPED>(a, large, grid, s);
+    else launch_shape<F, BF16, false, false, GROUPED>(a, large, grid, s);
+}
+
+template <bool GROUPED>
+void launch_all(plm_format f, bool bf16, const mfma_args& a, bool large, bool uniform, bool a8, dim3 grid,
+                hipStream_t s) {
+    if (f == PLM_INT4) {
+        if (bf16) launch_mode<PLM_INT4, true, GROUPED>(a, large, uniform, a8, grid, s);
+        else launch_mode<PLM_INT4, false, GROUPED>(a, large, uniform, a8, grid, s);
+    } else {
+        if (bf16) launch_mode<PLM_FP8, true, GROUPED>(a, large, uniform, a8, grid, s);
+        else launch_mode<PLM_FP8, false, GROUPED>(a, large, uniform, a8, grid, s);
+    }
+}
+
+void fill_common(mfma_args& a, const void* x, const void* w, const void* scale, plm_dtype scale_dtype, int64_t m,
+                 int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y) {
     const layout_dims d = make_dims(n, k, block_n, group_size);
-    mfma_args a{};
     a.x = static_cast<const uint16_t*>(x);
     a.w = static_cast<const uint8_t*>(w);
     a.scale = scale;
@@ -261,9 +394,21 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
     a.strips = static_cast<int>(d.strips);
     a.groups = static_cast<int>(d.groups);
     a.group_size = static_cast<int>(group_size);
+}
+}  // namespace
+
+int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
+                plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y,
+                void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq, const float* x_scale) {
+    const mfma_config c = choose_mfma(m, n, k);
+    mfma_args a{};
+    fill_common(a, x, w, scale, scale_dtype, m, n, k, block_n, group_size, y);
     a.splits = c.splits;
     a.tiles_per_split = c.tiles_per_split;
     a.m_blocks = c.m_blocks;
+    a.n_blocks = c.n_blocks;
+    a.xq = xq;
+    a.x_scale = x_scale;
     if (c.splits > 1) {
         const int64_t need = mfma_workspace_bytes(f, m, n, k);
         if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need) {
@@ -274,24 +419,34 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
         a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     }
     dim3 grid(c.m_blocks * c.n_blocks, c.splits);
-    const bool uniform = group_size % kTileK == 0;
-    auto go = [&](auto fmt_tag, auto bf_tag, auto uni_tag) {
-        mfma_kernel<decltype(fmt_tag)::value, decltype(bf_tag)::value, 128, decltype(uni_tag)::value>
-            <<<grid, kWaves * 64, 0, s>>>(a);
-    };
-    using I4 = std::integral_constant<plm_format, PLM_INT4>;
-    using F8 = std::integral_constant<plm_format, PLM_FP8>;
-    using T = std::true_type;
-    using Fa = std::false_type;
-    if (f == PLM_INT4) {
-        if (bf16) uniform ? go(I4{}, T{}, T{}) : go(I4{}, T{}, Fa{});
-        else uniform ? go(I4{}, Fa{}, T{}) : go(I4{}, Fa{}, Fa{});
-    } else {
-        if (bf16) uniform ? go(F8{}, T{}, T{}) : go(F8{}, T{}, Fa{});
-        else uniform ? go(F8{}, Fa{}, T{}) : go(F8{}, Fa{}, Fa{});
-    }
+    launch_all<false>(f, bf16, a, c.large, group_size % kTileK == 0, xq != nullptr, grid, s);
     PLM_HIP_LAUNCH_CHECK(op);
     return PLM_OK;
 }
+
+// Grouped: `tiles` holds max_tiles (expert, first row, rows) records built on the device;
+// rows are in the grouped (sorted) order and `row_index` optionally gathers them from x.
+int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
+                   plm_dtype scale_dtype, int64_t rows, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                   void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* row_index, bool large,
+                   hipStream_t s) {
+    mfma_args a{};
+    fill_common(a, x, w, scale, scale_dtype, rows, n, k, block_n, group_size, y);
+    const shape sh = large ? kLarge : kSmall;
+    a.splits = 1;
+    a.tiles_per_split = a.ktiles;
+    a.m_blocks = 1;
+    a.n_blocks = static_cast<int>(ceil_div(a.strips, sh.bs()));
+    a.tiles = tiles;
+    a.row_index = row_index;
+    a.w_expert_bytes = ceil_div(n, kTileN) * ceil_div(k, kTileK) * tile_bytes(f);
+    a.s_expert_bytes = static_cast<int64_t>(a.strips) * a.groups * a.scale_cols * dtype_size(scale_dtype);
+    dim3 grid(static_cast<unsigned>(max_tiles * a.n_blocks), 1);
+    launch_all<true>(f, bf16, a, large, group_size % kTileK == 0, false, grid, s);
+    PLM_HIP_LAUNCH_CHECK(op);
+    return PLM_OK;
+}
+
+int grouped_block_rows(bool large) { return large ? kLarge.bm() : kSmall.bm(); }
 
 }  // namespace plm

@@ -9,7 +9,7 @@
 #include <cstdio>
 #include <string>
 
-#include "../../include/pulsarlm_amd.h"
+#include "pulsarlm_amd.h"
 
 namespace plm {
 
@@ -79,6 +79,11 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
     }
+}
+
+typedef __attribute__((ext_vector_type(8))) uint32_t u32x8_t;
+__device__ __forceinline__ u32x8_t u32x8_cat(u32x4_t lo, u32x4_t hi) {
+    return u32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
 // 16x16x128 fp8 x fp8 (both OCP e4m3) MFMA, 32 bytes per lane per operand.
@@ -212,6 +217,44 @@ template <bool BF16> __device__ __forceinline__ u32x4_t dq_fp8(uint32_t lo, uint
     b[2] = pack2<BF16>(a2[0] * s, a2[1] * s);
     b[3] = pack2<BF16>(a3[0] * s, a3[1] * s);
     return b;
+}
+
+// Raw buffer loads: lanes whose offset is past num_records read 0 without a memory
+// access, which is how rows >= M, columns >= K and idle tiles are skipped for free.
+// Offsets at or past kOOB are outside every buffer the kernels build (checked on the host).
+constexpr int kOOB = 0x40000000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                             0x00020000);
+}
+__device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t r, int offset) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0));
+}
+// voffset (per lane) + soffset (wave-uniform, an SGPR).
+__device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+}
+__device__ __forceinline__ uint32_t buffer_load_u16(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, voffset, soffset, 0);
+}
+__device__ __forceinline__ uint32_t buffer_load_u32(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voffset, soffset, 0);
+}
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Scale bits as loaded (16-bit fp16/bf16 zero-extended, or fp32) -> fp32.
+template <bool WIDE> __device__ __forceinline__ float scale_from_bits(uint32_t bits, bool bf16_storage) {
+    if constexpr (WIDE) {
+        return __uint_as_float(bits);
+    } else {
+        const float as_bf16 = __uint_as_float(bits << 16);
+        const float as_f16 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+        return bf16_storage ? as_bf16 : as_f16;
+    }
+}
+template <bool WIDE> __device__ __forceinline__ uint32_t load_scale_bits(const void* base, int64_t index) {
+    if constexpr (WIDE) return static_cast<const uint32_t*>(base)[index];
+    else return static_cast<const uint16_t*>(base)[index];
 }
 
 // ---------------------------------------------------------------------------

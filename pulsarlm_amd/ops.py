@@ -195,3 +195,37 @@ def gemm_int4_marlin_cuda(x, weight_marlin, scale_marlin, n: int, block_n: int, 
 def gemm_fp8_marlin_cuda(x, weight_marlin, scale_marlin, n: int, block_n: int, group_size: int, out=None):
     """fp8 W8A16 form (ops.hpp:336-343; marlin.cu:642-651)."""
     return _gemm("gemm_fp8_marlin", _lib.PLM_FP8, x, weight_marlin, scale_marlin, n, block_n, group_size, out)
+
+
+def quantize_rows_e4m3_cuda(x: torch.Tensor):
+    """Per-row dynamic e4m3 quantization: (codes uint8 [M, K], scale fp32 [M]),
+    scale = max(amax, 1e-12) / 448 (the test_qwen3_5.cpp:301-311 rule per row)."""
+    op = "quantize_rows_e4m3"
+    _require(x.is_cuda and x.dtype in (torch.float16, torch.bfloat16), op, "x must be a CUDA fp16/bf16 tensor")
+    _require(x.dim() == 2 and x.is_contiguous(), op, "x must be a contiguous [M, K]")
+    m, k = x.shape
+    codes = torch.empty((m, k), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((m,), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        _call("plm_quantize_rows_e4m3", _ptr(x), _DTYPES[x.dtype], m, k, _ptr(codes), _ptr(scale),
+              _stream(x.device))
+    return codes, scale
+
+
+def gemm_fp8_w8a8_cuda(x, weight_marlin, scale_marlin, n: int, block_n: int, group_size: int, out=None):
+    """W8A8: x quantized per row to e4m3, fp8 x fp8 MFMA with fp32 block scales
+    (no reference counterpart; the reference's fp8 GEMM is W8A16)."""
+    op = "gemm_fp8_w8a8"
+    _gemm_checks(op, _lib.PLM_FP8, x, weight_marlin, scale_marlin, n, block_n, group_size)
+    _require(group_size % 128 == 0, op, "group_size must be a multiple of 128 for the fp8 MFMA")
+    m, k = x.shape
+    y = out if out is not None else torch.empty((m, n), dtype=x.dtype, device=x.device)
+    if m == 0 or n == 0:
+        return y
+    lib = _lib.load()
+    ws = workspace(x.device, lib.plm_gemm_w8a8_workspace_bytes(m, n, k))
+    with torch.cuda.device(x.device):
+        _call("plm_gemm_w8a8", _ptr(x), _DTYPES[x.dtype], _ptr(weight_marlin.contiguous()),
+              _ptr(scale_marlin.contiguous()), _DTYPES[scale_marlin.dtype], m, n, k, block_n, group_size, _ptr(y),
+              _ptr(ws), 0 if ws is None else ws.numel(), _stream(x.device))
+    return y

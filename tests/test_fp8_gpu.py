@@ -1,0 +1,71 @@
+"""fp8 paths on the GPU: per-row e4m3 activation quantization (bit-exact vs the
+oracle) and the W8A8 GEMM (tolerance vs the oracle's exact-product reference),
+plus W8A16 at the BASELINE config-4 shapes. The W8A8 mode has no reference
+counterpart: its parity is pinned only by the oracle restatement."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from pulsarlm_amd import ops
+from tests._util import TDT, assert_close, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("m,k", [(1, 128), (16, 5120), (37, 1040)])
+def test_quantize_rows_bit_exact(m, k, dtype):
+    rng = np.random.default_rng(m + k)
+    x = O.round_to(rng.standard_normal((m, k)).astype(np.float32) * np.exp2(rng.integers(-6, 6, (m, 1))), dtype)
+    x[0, :3] = 0.0
+    codes, scale = ops.quantize_rows_e4m3_cuda(to_dev(x, TDT[dtype]))
+    ref_codes, ref_scale = O.quantize_per_token_e4m3(x)
+    assert np.array_equal(scale.cpu().numpy(), ref_scale)
+    assert np.array_equal(codes.cpu().numpy(), ref_codes)
+
+
+def _fp8_weights(n, k, seed):
+    rng = np.random.default_rng(seed)
+    w = O.bf16_round(rng.standard_normal((n, k)).astype(np.float32) * 0.02)
+    codes, scale = O.fp8_block_quantize(w, 128, 128)
+    wt, st = ops.repack_fp8_marlin_cuda(to_dev(codes).view(torch.float8_e4m3fn), to_dev(scale), 128, 128)
+    return codes, scale, wt, st
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 300])
+def test_w8a8_matches_oracle(m, dtype):
+    n, k = 520, 1024
+    codes, scale, wt, st = _fp8_weights(n, k, seed=m)
+    x = O.round_to(np.random.default_rng(m).standard_normal((m, k)).astype(np.float32), dtype)
+    y = ops.gemm_fp8_w8a8_cuda(to_dev(x, TDT[dtype]), wt, st, n, 128, 128)
+    xc, xs = O.quantize_per_token_e4m3(x)
+    ref = O.gemm_w8a8_ref(xc, xs, codes, scale, 128, 128, dtype=None)
+    assert_close(y, ref, f"w8a8 m={m}")
+
+
+@pytest.mark.parametrize("shape", [(5120, 7168), (5120, 5120), (5120, 34816), (17408, 5120)])
+@pytest.mark.parametrize("m", [1, 16, 2048])
+def test_config4_qwen3_27b_shapes(shape, m):
+    """fp8 128x128 block weights, W8A16 (bf16 x) and W8A8."""
+    k, n = shape
+    codes, scale, wt, st = _fp8_weights(n, k, seed=k + n)
+    x = O.bf16_round(np.random.default_rng(m).standard_normal((m, k)).astype(np.float32))
+    xd = to_dev(x, torch.bfloat16)
+    w_deq = O.dequant_fp8(codes, scale, 128, 128)
+    rows = slice(0, min(m, 64))  # the CPU reference on a row sample at M=2048
+    y = ops.gemm_fp8_marlin_cuda(xd, wt, st, n, 128, 128)
+    assert_close(y[rows], O.gemm_ref(x[rows], w_deq, None), f"w8a16 {shape} m={m}")
+    y8 = ops.gemm_fp8_w8a8_cuda(xd, wt, st, n, 128, 128)
+    xc, xs = O.quantize_per_token_e4m3(x[rows])
+    assert_close(y8[rows], O.gemm_w8a8_ref(xc, xs, codes, scale, 128, 128, dtype=None), f"w8a8 {shape} m={m}")
+
+
+def test_w8a8_rejects_small_groups():
+    codes = np.zeros((64, 256), np.uint8)
+    wt, st = ops.repack_fp8_marlin_cuda(to_dev(codes).view(torch.float8_e4m3fn),
+                                        torch.ones((1, 4), device="cuda"), 128, 64)
+    with pytest.raises(RuntimeError, match="gemm_fp8_w8a8: group_size must be a multiple of 128"):
+        ops.gemm_fp8_w8a8_cuda(torch.zeros((4, 256), dtype=torch.bfloat16, device="cuda"), wt, st, 64, 128, 64)
