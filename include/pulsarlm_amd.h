@@ -152,13 +152,16 @@ int plm_gemm_w8a8(const void* x, plm_dtype x_dtype,
  * expert e's weight. weight holds n_experts repacked [N, K] matrices back to
  * back (plm_weight_bytes each), scale likewise (plm_scale_bytes each).
  * Replaces one at::_grouped_mm(rows, W^T, offsets) call of routed_experts
- * (paged_forward.cpp:124-125) for int4 experts.
+ * (paged_forward.cpp:124-125) for int4 experts (PLM_INT4 only).
  */
 int plm_grouped_gemm(plm_format format, const void* x, plm_dtype x_dtype,
                      const void* weight, const void* scale, plm_dtype scale_dtype,
                      const int32_t* offsets, int64_t n_experts, int64_t rows,
                      int64_t n, int64_t k, int64_t block_n, int64_t group_size,
                      void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes plm_grouped_gemm needs for `rows` rows over n_experts experts. */
+int64_t plm_grouped_gemm_workspace_bytes(int64_t rows, int64_t n_experts);
 
 /* Workspace bytes plm_moe needs. */
 int64_t plm_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t n_experts,
@@ -171,12 +174,15 @@ int64_t plm_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t n_experts
  * gate_up holds n_experts repacked [2I, H] weights, down n_experts [H, I].
  * Sorting by expert, offsets, gather, both grouped GEMMs, the activation and the
  * weighted scatter-back all run on the device with no host synchronization.
+ * offsets (int32 [n_experts], written) receives the inclusive-end row offsets of
+ * the stable sort, as at::cumsum(counts) in the reference. Stable and deterministic:
+ * the same inputs give the same bits.
  */
 int plm_moe(const void* h, plm_dtype dtype, const int32_t* top_experts, const float* top_weights,
             int64_t tokens, int64_t top_k, int64_t n_experts, int64_t hidden, int64_t intermediate,
             const void* gate_up_weight, const void* gate_up_scale,
             const void* down_weight, const void* down_scale, plm_dtype scale_dtype, int64_t group_size,
-            void* out, void* workspace, size_t workspace_bytes, void* stream);
+            int32_t* offsets, void* out, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

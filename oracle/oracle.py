@@ -371,10 +371,12 @@ def moe_sort(top_experts, n_experts: int):
 
 def routed_experts_ref(h, top_experts, top_weights, gate_up, down, dtype="bf16"):
     """Restatement of routed_experts with dense per-expert weights (already
-    dequantized): gate_up [E, 2I, H], down [E, H, I]. Each GEMM accumulates in
-    float64 and rounds its output to ``dtype``, as the grouped GEMM's bf16
-    output does; silu(g)*u is rounded to ``dtype`` before the down GEMM; the
-    scatter-back sums in float64 and rounds once."""
+    dequantized): gate_up [E, 2I, H], down [E, H, I], with the reference's
+    rounding points in the activation dtype: each grouped GEMM's output
+    (accumulated here in float64), at::silu(g), its product with u, and each
+    weighted term down * top_weight.to(dtype) (paged_forward.cpp:124-128). The
+    reference's index_add_ accumulates those terms in the activation dtype in a
+    scheduling-dependent order; here they are summed in float64 and rounded once."""
     h = np.asarray(h, dtype=np.float32)
     e_count = gate_up.shape[0]
     inter = gate_up.shape[1] // 2
@@ -388,9 +390,10 @@ def routed_experts_ref(h, top_experts, top_weights, gate_up, down, dtype="bf16")
         if end > start:
             r = rows[start:end]
             gu = gemm_ref(r, gate_up[e], dtype)
-            act = round_to(silu(gu[:, :inter]) * gu[:, inter:], dtype)
-            d = gemm_ref(act, down[e], dtype).astype(np.float64)
-            np.add.at(out, tokens[start:end], d * round_to(wflat[start:end], dtype)[:, None])
+            act = round_to(round_to(silu(gu[:, :inter]), dtype) * gu[:, inter:], dtype)
+            d = gemm_ref(act, down[e], dtype)
+            term = round_to(d * round_to(wflat[start:end], dtype)[:, None], dtype)
+            np.add.at(out, tokens[start:end], term.astype(np.float64))
         start = end
     return round_to(out.astype(np.float32), dtype)
 
@@ -411,9 +414,9 @@ def sparse_moe_ref(h, top_experts, top_weights, gate_up, down, dtype="bf16"):
             continue
         weight = (tw * chosen).sum(-1)[toks]
         gu = gemm_ref(h[toks], gate_up[e], dtype)
-        act = round_to(silu(gu[:, :inter]) * gu[:, inter:], dtype)
-        d = gemm_ref(act, down[e], dtype).astype(np.float64)
-        out[toks] += d * round_to(weight, dtype)[:, None]
+        act = round_to(round_to(silu(gu[:, :inter]), dtype) * gu[:, inter:], dtype)
+        d = gemm_ref(act, down[e], dtype)
+        out[toks] += round_to(d * round_to(weight, dtype)[:, None], dtype).astype(np.float64)
     return round_to(out.astype(np.float32), dtype)
 
 

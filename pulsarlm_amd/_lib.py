@@ -34,8 +34,10 @@ SIGNATURES = {
     "plm_gemm_w8a8": (_INT, [_P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ, _P]),
     "plm_grouped_gemm": (_INT, [_INT, _P, _INT, _P, _P, _INT, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ,
                                 _P]),
+    "plm_grouped_gemm_workspace_bytes": (_I64, [_I64, _I64]),
     "plm_moe_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
-    "plm_moe": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _INT, _I64, _P, _P, _SZ, _P]),
+    "plm_moe": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _INT, _I64, _P, _P, _P, _SZ,
+                       _P]),
 }
 
 _lib = None

@@ -142,17 +142,3 @@ int plm_gemm_w8a8(const void* x, plm_dtype x_dtype, const void* weight, const vo
 
 }  // extern "C"
 
-// Entry points whose kernels are not built yet report so instead of running.
-extern "C" {
-int plm_grouped_gemm(plm_format, const void*, plm_dtype, const void*, const void*, plm_dtype, const int32_t*, int64_t,
-                     int64_t, int64_t, int64_t, int64_t, int64_t, void*, void*, size_t, void*) {
-    plm::set_error("grouped_gemm", "not implemented");
-    return PLM_ERR_INVALID;
-}
-int64_t plm_moe_workspace_bytes(int64_t, int64_t, int64_t, int64_t, int64_t) { return 0; }
-int plm_moe(const void*, plm_dtype, const int32_t*, const float*, int64_t, int64_t, int64_t, int64_t, int64_t,
-            const void*, const void*, const void*, const void*, plm_dtype, int64_t, void*, void*, size_t, void*) {
-    plm::set_error("routed_experts", "not implemented");
-    return PLM_ERR_INVALID;
-}
-}

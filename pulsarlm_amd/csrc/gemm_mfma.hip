@@ -26,6 +26,7 @@
 //   scales are found at a fixed stride.
 // * Split-K across workgroups when the output has too few tiles to fill the GPU, reduced
 //   deterministically by the last workgroup to arrive.
+#include <algorithm>
 #include <type_traits>
 
 #include "plm_common.hpp"
@@ -310,6 +311,10 @@ struct shape {
 };
 constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts (one per SIMD, 512 registers)
 constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
+// Grouped calls also use short row blocks for experts with few rows.
+constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
+constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
+constexpr shape kGroupedShapes[4] = {kRows16, kRows64, kSmall, kLarge};
 
 }  // namespace
 
@@ -426,13 +431,48 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
 
 // Grouped: `tiles` holds max_tiles (expert, first row, rows) records built on the device;
 // rows are in the grouped (sorted) order and `row_index` optionally gathers them from x.
+// shape indexes kGroupedShapes (int4 experts only).
+namespace {
+template <bool BF16, bool UNIFORM>
+void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
+#define PLM_GROUPED_CASE(i)                                                                                   \
+    case i:                                                                                                   \
+        mfma_kernel<PLM_INT4, BF16, UNIFORM, false, true, kGroupedShapes[i].wm, kGroupedShapes[i].wn,         \
+                    kGroupedShapes[i].mt, kGroupedShapes[i].ns>                                               \
+            <<<grid, kGroupedShapes[i].wm * kGroupedShapes[i].wn * 64, 0, s>>>(a);                            \
+        break;
+    switch (shape) {
+        PLM_GROUPED_CASE(0)
+        PLM_GROUPED_CASE(1)
+        PLM_GROUPED_CASE(2)
+        default:
+            mfma_kernel<PLM_INT4, BF16, UNIFORM, false, true, kLarge.wm, kLarge.wn, kLarge.mt, kLarge.ns>
+                <<<grid, kLarge.wm * kLarge.wn * 64, 0, s>>>(a);
+    }
+#undef PLM_GROUPED_CASE
+}
+}  // namespace
+
+int grouped_block_rows(int shape) { return kGroupedShapes[std::min(std::max(shape, 0), 3)].bm(); }
+
+// Row block for a grouped call: about the average rows per expert.
+int grouped_shape_for(int64_t rows, int64_t n_experts) {
+    const int64_t avg = ceil_div(rows, std::max<int64_t>(n_experts, 1));
+    if (avg <= 24) return 0;
+    if (avg <= 96) return 1;
+    if (avg <= 192) return 2;
+    return 3;
+}
+
 int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                    plm_dtype scale_dtype, int64_t rows, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
-                   void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* row_index, bool large,
+                   void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* row_index, int shape,
                    hipStream_t s) {
+    PLM_CHECK_ARG(f == PLM_INT4, op, "grouped GEMMs take int4 experts");
+    PLM_CHECK_ARG(rows < (int64_t{1} << 31) / 2 && n * k < (int64_t{1} << 40), op, "problem too large");
     mfma_args a{};
     fill_common(a, x, w, scale, scale_dtype, rows, n, k, block_n, group_size, y);
-    const shape sh = large ? kLarge : kSmall;
+    const struct shape sh = kGroupedShapes[std::min(std::max(shape, 0), 3)];
     a.splits = 1;
     a.tiles_per_split = a.ktiles;
     a.m_blocks = 1;
@@ -442,11 +482,11 @@ int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const
     a.w_expert_bytes = ceil_div(n, kTileN) * ceil_div(k, kTileK) * tile_bytes(f);
     a.s_expert_bytes = static_cast<int64_t>(a.strips) * a.groups * a.scale_cols * dtype_size(scale_dtype);
     dim3 grid(static_cast<unsigned>(max_tiles * a.n_blocks), 1);
-    launch_all<true>(f, bf16, a, large, group_size % kTileK == 0, false, grid, s);
+    const bool uniform = group_size % kTileK == 0;
+    if (bf16) uniform ? launch_grouped_shape<true, true>(a, shape, grid, s) : launch_grouped_shape<true, false>(a, shape, grid, s);
+    else uniform ? launch_grouped_shape<false, true>(a, shape, grid, s) : launch_grouped_shape<false, false>(a, shape, grid, s);
     PLM_HIP_LAUNCH_CHECK(op);
     return PLM_OK;
 }
-
-int grouped_block_rows(bool large) { return large ? kLarge.bm() : kSmall.bm(); }
 
 }  // namespace plm

@@ -1,0 +1,331 @@
+// Grouped GEMM over experts and the routed-experts MoE block, all on the device with no
+// host synchronization.
+//
+// Counterpart of routed_experts (pulsarlm-core/src/engine/model/paged_forward.cpp:108-130):
+//   stable argsort of the (token, k) assignments by expert, counts, int32 inclusive-end
+//   offsets (at::cumsum), gathered rows, at::_grouped_mm(rows, gate_up^T, offsets),
+//   act(g) * u, at::_grouped_mm(..., down^T, offsets), x top weight, index_add_ into [T, H].
+// Here the experts are int4 (plm layout) and the GEMMs are the grouped MFMA kernel:
+// * sort: a counting sort in three small kernels -- per-chunk histograms, a per-expert
+//   scan over chunks, and a scatter in which each assignment's rank among the earlier
+//   assignments of its expert in its chunk is counted directly -- stable and
+//   deterministic, unlike the atomics of a GPU index_add_;
+// * the gate_up GEMM gathers its A rows through the sorted token index instead of
+//   materializing the gathered rows;
+// * the scatter-back is a gather: each token sums its top_k weighted expert outputs in k
+//   order in fp32 and rounds once, so the result does not depend on scheduling.
+#include <algorithm>
+
+#include "plm_common.hpp"
+
+namespace plm {
+
+int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
+                   plm_dtype scale_dtype, int64_t rows, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                   void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* row_index, int shape,
+                   hipStream_t s);
+int grouped_block_rows(int shape);
+int grouped_shape_for(int64_t rows, int64_t n_experts);
+
+namespace {
+
+constexpr int kChunk = 256;  // assignments per sort chunk
+
+// Per-chunk expert histogram: counts[chunk][e].
+__global__ void __launch_bounds__(kChunk) moe_hist_kernel(const int32_t* __restrict__ experts, int64_t total,
+                                                          int n_experts, int32_t* __restrict__ counts) {
+    extern __shared__ int32_t hist[];
+    for (int e = threadIdx.x; e < n_experts; e += kChunk) hist[e] = 0;
+    __syncthreads();
+    const int64_t a = static_cast<int64_t>(blockIdx.x) * kChunk + threadIdx.x;
+    if (a < total) {
+        const int e = experts[a];
+        if (e >= 0 && e < n_experts) atomicAdd(&hist[e], 1);  // integer counts: order does not matter
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < n_experts; e += kChunk) counts[static_cast<int64_t>(blockIdx.x) * n_experts + e] = hist[e];
+}
+
+// One workgroup: per expert, exclusive scan over chunks (in place) and the total; then
+// an exclusive scan over experts for the start rows, and the inclusive-end offsets.
+__global__ void __launch_bounds__(1024) moe_scan_kernel(int32_t* __restrict__ counts, int n_chunks, int n_experts,
+                                                         int32_t* __restrict__ start, int32_t* __restrict__ offsets) {
+    extern __shared__ int32_t tot[];
+    for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
+        int32_t run = 0;
+        for (int c = 0; c < n_chunks; ++c) {
+            const int32_t v = counts[static_cast<int64_t>(c) * n_experts + e];
+            counts[static_cast<int64_t>(c) * n_experts + e] = run;
+            run += v;
+        }
+        tot[e] = run;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t run = 0;
+        for (int e = 0; e < n_experts; ++e) {
+            start[e] = run;
+            run += tot[e];
+            offsets[e] = run;
+        }
+    }
+}
+
+// Scatter: sorted position of every assignment, the token it reads and its weight.
+__global__ void __launch_bounds__(kChunk) moe_scatter_kernel(const int32_t* __restrict__ experts,
+                                                             const float* __restrict__ weights, int64_t total, int top_k,
+                                                             int n_experts, const int32_t* __restrict__ chunk_base,
+                                                             const int32_t* __restrict__ start,
+                                                             int32_t* __restrict__ sorted_token,
+                                                             float* __restrict__ sorted_weight,
+                                                             int32_t* __restrict__ position) {
+    __shared__ int32_t chunk_experts[kChunk];
+    const int64_t a = static_cast<int64_t>(blockIdx.x) * kChunk + threadIdx.x;
+    const int e = a < total ? experts[a] : -1;
+    chunk_experts[threadIdx.x] = e;
+    __syncthreads();
+    if (a >= total || e < 0 || e >= n_experts) return;
+    int rank = 0;
+    for (int j = 0; j < static_cast<int>(threadIdx.x); ++j) rank += chunk_experts[j] == e;
+    const int32_t pos = start[e] + chunk_base[static_cast<int64_t>(blockIdx.x) * n_experts + e] + rank;
+    sorted_token[pos] = static_cast<int32_t>(a / top_k);
+    sorted_weight[pos] = weights[a];
+    position[a] = pos;
+}
+
+// Tile list for the grouped GEMM: expert e's rows [off[e-1], off[e]) in blocks of bm,
+// written at the expert's tile prefix; slots past the last tile get rows = 0.
+__global__ void __launch_bounds__(1024) moe_tiles_kernel(const int32_t* __restrict__ offsets, int n_experts, int bm,
+                                                          int64_t max_tiles, int32_t* __restrict__ tiles) {
+    extern __shared__ int32_t first_tile[];
+    if (threadIdx.x == 0) {
+        int32_t run = 0, prev = 0;
+        for (int e = 0; e < n_experts; ++e) {
+            first_tile[e] = run;
+            const int32_t rows = offsets[e] - prev;
+            prev = offsets[e];
+            run += rows > 0 ? (rows + bm - 1) / bm : 0;
+        }
+        first_tile[n_experts] = run;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
+        const int32_t lo = e == 0 ? 0 : offsets[e - 1], hi = offsets[e];
+        int32_t t = first_tile[e];
+        for (int32_t r = lo; r < hi; r += bm, ++t) {
+            tiles[3 * t] = e;
+            tiles[3 * t + 1] = r;
+            tiles[3 * t + 2] = min(bm, hi - r);
+        }
+    }
+    for (int64_t t = first_tile[n_experts] + threadIdx.x; t < max_tiles; t += blockDim.x) {
+        tiles[3 * t] = 0;
+        tiles[3 * t + 1] = 0;
+        tiles[3 * t + 2] = 0;
+    }
+}
+
+// act[r, i] = round(round(silu(g)) * u) with (g | u) = gu[r, :] (the reference's
+// at::silu(gate) * up in the activation dtype).
+template <bool BF16>
+__global__ void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t rows, int inter, uint16_t* __restrict__ act) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= rows * inter) return;
+    const int64_t r = i / inter, c = i % inter;
+    const float g = from_bits16<BF16>(gu[r * 2 * inter + c]);
+    const float u = from_bits16<BF16>(gu[r * 2 * inter + inter + c]);
+    const float sg = round_to<BF16>(g / (1.f + __expf(-g)));
+    act[i] = static_cast<uint16_t>(to_bits16<BF16>(sg * u));
+}
+
+// out[t, h] = sum_j round(d[pos(t, j), h] * round(w[t, j])), summed in j order in fp32.
+template <bool BF16>
+__global__ void moe_combine_kernel(const uint16_t* __restrict__ d, const int32_t* __restrict__ position,
+                                   const float* __restrict__ weights, int64_t tokens, int top_k, int hidden,
+                                   uint16_t* __restrict__ out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= tokens * hidden) return;
+    const int64_t t = i / hidden, h = i % hidden;
+    float acc = 0.f;
+    for (int j = 0; j < top_k; ++j) {
+        const int32_t p = position[t * top_k + j];
+        const float w = round_to<BF16>(weights[t * top_k + j]);
+        acc += round_to<BF16>(from_bits16<BF16>(d[static_cast<int64_t>(p) * hidden + h]) * w);
+    }
+    out[i] = static_cast<uint16_t>(to_bits16<BF16>(acc));
+}
+
+struct moe_ws {
+    int64_t counts, start, sorted_token, sorted_weight, position, tiles, gu, act, d, total;
+};
+
+int64_t align256(int64_t v) { return round_up(v, 256); }
+
+moe_ws moe_layout(int64_t tokens, int64_t top_k, int64_t n_experts, int64_t hidden, int64_t inter, int64_t max_tiles) {
+    const int64_t rows = tokens * top_k;
+    const int64_t chunks = ceil_div(rows, kChunk);
+    moe_ws w{};
+    int64_t off = kCounterBytes;  // the split-K counter region stays at the front
+    auto take = [&](int64_t bytes) {
+        const int64_t at = off;
+        off += align256(std::max<int64_t>(bytes, 1));
+        return at;
+    };
+    w.counts = take(chunks * n_experts * 4);
+    w.start = take(n_experts * 4);
+    w.sorted_token = take(rows * 4);
+    w.sorted_weight = take(rows * 4);
+    w.position = take(rows * 4);
+    w.tiles = take(max_tiles * 12);
+    w.gu = take(rows * 2 * inter * 2);
+    w.act = take(rows * inter * 2);
+    w.d = take(rows * hidden * 2);
+    w.total = off;
+    return w;
+}
+
+int64_t moe_max_tiles(int64_t rows, int64_t n_experts) {
+    const int bm = grouped_block_rows(grouped_shape_for(rows, n_experts));
+    return ceil_div(rows, bm) + n_experts;
+}
+
+int launch_sort(const char* op, const int32_t* experts, const float* weights, int64_t rows, int64_t top_k,
+                int64_t n_experts, uint8_t* base, const moe_ws& l, int32_t* offsets, hipStream_t s) {
+    const int64_t chunks = ceil_div(rows, kChunk);
+    auto* counts = reinterpret_cast<int32_t*>(base + l.counts);
+    auto* start = reinterpret_cast<int32_t*>(base + l.start);
+    const size_t hist_lds = static_cast<size_t>(n_experts) * 4;
+    moe_hist_kernel<<<static_cast<unsigned>(chunks), kChunk, hist_lds, s>>>(experts, rows, int(n_experts), counts);
+    moe_scan_kernel<<<1, 1024, hist_lds, s>>>(counts, int(chunks), int(n_experts), start, offsets);
+    moe_scatter_kernel<<<static_cast<unsigned>(chunks), kChunk, 0, s>>>(
+        experts, weights, rows, int(top_k), int(n_experts), counts, start,
+        reinterpret_cast<int32_t*>(base + l.sorted_token), reinterpret_cast<float*>(base + l.sorted_weight),
+        reinterpret_cast<int32_t*>(base + l.position));
+    PLM_HIP_LAUNCH_CHECK(op);
+    return PLM_OK;
+}
+
+int launch_tiles(const char* op, const int32_t* offsets, int64_t n_experts, int bm, int64_t max_tiles, int32_t* tiles,
+                 hipStream_t s) {
+    moe_tiles_kernel<<<1, 1024, static_cast<size_t>(n_experts + 1) * 4, s>>>(offsets, int(n_experts), bm, max_tiles,
+                                                                              tiles);
+    PLM_HIP_LAUNCH_CHECK(op);
+    return PLM_OK;
+}
+
+}  // namespace
+}  // namespace plm
+
+using namespace plm;
+
+extern "C" {
+
+int plm_grouped_gemm(plm_format format, const void* x, plm_dtype x_dtype, const void* weight, const void* scale,
+                     plm_dtype scale_dtype, const int32_t* offsets, int64_t n_experts, int64_t rows, int64_t n,
+                     int64_t k, int64_t block_n, int64_t group_size, void* y, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+    const char* op = "grouped_gemm";
+    clear_error();
+    PLM_CHECK_ARG(format == PLM_INT4 || format == PLM_FP8, op, "unknown weight format");
+    PLM_CHECK_ARG(x_dtype == PLM_BF16 || x_dtype == PLM_FP16, op, "x must be fp16 or bf16");
+    PLM_CHECK_ARG(scale_dtype == PLM_BF16 || scale_dtype == PLM_FP16 || scale_dtype == PLM_FP32, op,
+                  "scale dtype must be bf16, fp16 or fp32");
+    PLM_CHECK_ARG(n_experts > 0 && n_experts <= 4096, op, "n_experts must be in [1, 4096]");
+    PLM_CHECK_ARG(rows >= 0 && n >= 0 && k >= 0 && block_n > 0, op, "bad sizes");
+    PLM_CHECK_ARG(group_size > 0 && group_size % 16 == 0 && k % group_size == 0, op,
+                  "group_size must be a positive multiple of 16 dividing K");
+    if (rows == 0 || n == 0) return PLM_OK;
+    PLM_CHECK_ARG(x && weight && scale && offsets && y, op, "null pointer");
+    PLM_CHECK_ARG(aligned(x, 16) && aligned(weight, 16), op, "x and weight must be 16-byte aligned");
+    const int shape = grouped_shape_for(rows, n_experts);
+    const int64_t max_tiles = ceil_div(rows, grouped_block_rows(shape)) + n_experts;
+    const int64_t need = kCounterBytes + max_tiles * 12;
+    if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need) {
+        set_error(op, "workspace of %lld bytes required, %zu given", static_cast<long long>(need), workspace_bytes);
+        return PLM_ERR_WORKSPACE;
+    }
+    auto* tiles = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + kCounterBytes);
+    hipStream_t s = as_stream(stream);
+    if (int rc = launch_tiles(op, offsets, n_experts, grouped_block_rows(shape), max_tiles, tiles, s)) return rc;
+    return launch_grouped(op, format, x, x_dtype == PLM_BF16, weight, scale, scale_dtype, rows, n, k, block_n,
+                          group_size, y, tiles, max_tiles, nullptr, shape, s);
+}
+
+int64_t plm_grouped_gemm_workspace_bytes(int64_t rows, int64_t n_experts) {
+    if (rows <= 0 || n_experts <= 0) return kCounterBytes;
+    const int shape = grouped_shape_for(rows, n_experts);
+    return kCounterBytes + (ceil_div(rows, grouped_block_rows(shape)) + n_experts) * 12;
+}
+
+int64_t plm_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t n_experts, int64_t hidden,
+                                int64_t intermediate) {
+    if (tokens <= 0 || top_k <= 0 || n_experts <= 0) return kCounterBytes;
+    const int64_t rows = tokens * top_k;
+    return moe_layout(tokens, top_k, n_experts, hidden, intermediate, moe_max_tiles(rows, n_experts)).total;
+}
+
+int plm_moe(const void* h, plm_dtype dtype, const int32_t* top_experts, const float* top_weights, int64_t tokens,
+            int64_t top_k, int64_t n_experts, int64_t hidden, int64_t intermediate, const void* gate_up_weight,
+            const void* gate_up_scale, const void* down_weight, const void* down_scale, plm_dtype scale_dtype,
+            int64_t group_size, int32_t* offsets, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+    const char* op = "routed_experts";
+    clear_error();
+    PLM_CHECK_ARG(dtype == PLM_BF16 || dtype == PLM_FP16, op, "h must be fp16 or bf16");
+    PLM_CHECK_ARG(scale_dtype == PLM_BF16 || scale_dtype == PLM_FP16 || scale_dtype == PLM_FP32, op,
+                  "scale dtype must be bf16, fp16 or fp32");
+    PLM_CHECK_ARG(tokens >= 0 && top_k > 0 && n_experts > 0 && n_experts <= 4096, op, "bad routing sizes");
+    PLM_CHECK_ARG(hidden > 0 && intermediate > 0, op, "hidden and intermediate must be positive");
+    PLM_CHECK_ARG(group_size > 0 && group_size % 16 == 0 && hidden % group_size == 0 && intermediate % group_size == 0,
+                  op, "group_size must be a positive multiple of 16 dividing hidden and intermediate");
+    PLM_CHECK_ARG(tokens * top_k <= (int64_t{1} << 30), op, "too many assignments");
+    if (tokens == 0) return PLM_OK;
+    PLM_CHECK_ARG(h && top_experts && top_weights && gate_up_weight && gate_up_scale && down_weight && down_scale &&
+                      offsets && out,
+                  op, "null pointer");
+    const int64_t rows = tokens * top_k;
+    const int64_t max_tiles = moe_max_tiles(rows, n_experts);
+    const moe_ws l = moe_layout(tokens, top_k, n_experts, hidden, intermediate, max_tiles);
+    if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < l.total) {
+        set_error(op, "workspace of %lld bytes required, %zu given", static_cast<long long>(l.total), workspace_bytes);
+        return PLM_ERR_WORKSPACE;
+    }
+    auto* base = static_cast<uint8_t*>(workspace);
+    hipStream_t s = as_stream(stream);
+    const bool bf16 = dtype == PLM_BF16;
+    const int shape = grouped_shape_for(rows, n_experts);
+    auto* tiles = reinterpret_cast<int32_t*>(base + l.tiles);
+    if (int rc = launch_sort(op, top_experts, top_weights, rows, top_k, n_experts, base, l, offsets, s)) return rc;
+    if (int rc = launch_tiles(op, offsets, n_experts, grouped_block_rows(shape), max_tiles, tiles, s)) return rc;
+    // gate_up: [rows, 2I] = h[sorted_token] @ gate_up_e^T
+    if (int rc = launch_grouped(op, PLM_INT4, h, bf16, gate_up_weight, gate_up_scale, scale_dtype, rows,
+                                2 * intermediate, hidden, 1, group_size, base + l.gu, tiles, max_tiles,
+                                reinterpret_cast<const int32_t*>(base + l.sorted_token), shape, s))
+        return rc;
+    const int64_t act_n = rows * intermediate;
+    if (bf16)
+        silu_mul_kernel<true><<<static_cast<unsigned>(ceil_div(act_n, 256)), 256, 0, s>>>(
+            reinterpret_cast<const uint16_t*>(base + l.gu), rows, int(intermediate),
+            reinterpret_cast<uint16_t*>(base + l.act));
+    else
+        silu_mul_kernel<false><<<static_cast<unsigned>(ceil_div(act_n, 256)), 256, 0, s>>>(
+            reinterpret_cast<const uint16_t*>(base + l.gu), rows, int(intermediate),
+            reinterpret_cast<uint16_t*>(base + l.act));
+    PLM_HIP_LAUNCH_CHECK(op);
+    // down: [rows, H] = act @ down_e^T
+    if (int rc = launch_grouped(op, PLM_INT4, base + l.act, bf16, down_weight, down_scale, scale_dtype, rows, hidden,
+                                intermediate, 1, group_size, base + l.d, tiles, max_tiles, nullptr, shape, s))
+        return rc;
+    const int64_t out_n = tokens * hidden;
+    if (bf16)
+        moe_combine_kernel<true><<<static_cast<unsigned>(ceil_div(out_n, 256)), 256, 0, s>>>(
+            reinterpret_cast<const uint16_t*>(base + l.d), reinterpret_cast<const int32_t*>(base + l.position),
+            top_weights, tokens, int(top_k), int(hidden), static_cast<uint16_t*>(out));
+    else
+        moe_combine_kernel<false><<<static_cast<unsigned>(ceil_div(out_n, 256)), 256, 0, s>>>(
+            reinterpret_cast<const uint16_t*>(base + l.d), reinterpret_cast<const int32_t*>(base + l.position),
+            top_weights, tokens, int(top_k), int(hidden), static_cast<uint16_t*>(out));
+    PLM_HIP_LAUNCH_CHECK(op);
+    return PLM_OK;
+}
+
+}  // extern "C"

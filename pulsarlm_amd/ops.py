@@ -229,3 +229,69 @@ def gemm_fp8_w8a8_cuda(x, weight_marlin, scale_marlin, n: int, block_n: int, gro
               _ptr(scale_marlin.contiguous()), _DTYPES[scale_marlin.dtype], m, n, k, block_n, group_size, _ptr(y),
               _ptr(ws), 0 if ws is None else ws.numel(), _stream(x.device))
     return y
+
+
+# ---------------------------------------------------------------------------
+# MoE: experts repacked back to back, grouped GEMM, routed experts
+# ---------------------------------------------------------------------------
+
+
+def repack_int4_experts(weight_packed: torch.Tensor, weight_scale: torch.Tensor, group_size: int):
+    """[E, N, K/8] int32 + [E, N, K/g] scales -> per-expert plm layouts back to back:
+    (weights int32 [E * words], scales [E, strips, groups, 16])."""
+    op = "repack_int4_experts"
+    _require(weight_packed.dim() == 3 and weight_scale.dim() == 3, op, "expected [E, N, K/8] and [E, N, K/g]")
+    e = weight_packed.shape[0]
+    ws, ss = [], []
+    for i in range(e):
+        w, s = repack_int4_marlin_cuda(weight_packed[i], weight_scale[i], 1, group_size)
+        ws.append(w)
+        ss.append(s)
+    return torch.cat(ws), torch.stack(ss)
+
+
+def grouped_gemm_int4_cuda(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, offsets: torch.Tensor, n: int,
+                           group_size: int, out=None) -> torch.Tensor:
+    """Rows [offsets[e-1], offsets[e]) of x times expert e's W^T (one at::_grouped_mm of
+    paged_forward.cpp:124-125, int4 experts)."""
+    op = "grouped_gemm"
+    _require(x.is_cuda and x.dim() == 2 and x.is_contiguous() and x.dtype in (torch.float16, torch.bfloat16), op,
+             "x must be a contiguous CUDA [rows, K] fp16/bf16")
+    _require(offsets.dtype == torch.int32 and offsets.dim() == 1, op, "offsets must be int32 [E]")
+    rows, k = x.shape
+    e = offsets.shape[0]
+    lib = _lib.load()
+    _require(weight.numel() * 4 == e * lib.plm_weight_bytes(_lib.PLM_INT4, n, k), op, "weight has the wrong size")
+    y = out if out is not None else torch.empty((rows, n), dtype=x.dtype, device=x.device)
+    if rows == 0 or n == 0:
+        return y
+    ws = workspace(x.device, lib.plm_grouped_gemm_workspace_bytes(rows, e))
+    with torch.cuda.device(x.device):
+        _call("plm_grouped_gemm", _lib.PLM_INT4, _ptr(x), _DTYPES[x.dtype], _ptr(weight), _ptr(scale),
+              _DTYPES[scale.dtype], _ptr(offsets.contiguous()), e, rows, n, k, 1, group_size, _ptr(y), _ptr(ws),
+              ws.numel(), _stream(x.device))
+    return y
+
+
+def routed_experts_int4_cuda(h: torch.Tensor, top_experts: torch.Tensor, top_weights: torch.Tensor,
+                             gate_up: tuple, down: tuple, intermediate: int, group_size: int):
+    """routed_experts (paged_forward.cpp:108-130) with int4 experts and SiLU:
+    returns (out [T, H] in h's dtype, offsets int32 [E])."""
+    op = "routed_experts"
+    _require(h.is_cuda and h.dim() == 2 and h.dtype in (torch.float16, torch.bfloat16), op,
+             "h must be a CUDA [T, H] fp16/bf16 tensor")
+    t, hidden = h.shape
+    top_k = top_experts.shape[-1]
+    e = gate_up[1].shape[0]
+    experts = top_experts.to(torch.int32).contiguous()
+    weights = top_weights.to(torch.float32).contiguous()
+    out = torch.empty_like(h)
+    offsets = torch.empty((e,), dtype=torch.int32, device=h.device)
+    lib = _lib.load()
+    ws = workspace(h.device, lib.plm_moe_workspace_bytes(t, top_k, e, hidden, intermediate))
+    with torch.cuda.device(h.device):
+        _call("plm_moe", _ptr(h.contiguous()), _DTYPES[h.dtype], _ptr(experts), _ptr(weights), t, top_k, e, hidden,
+              intermediate, _ptr(gate_up[0]), _ptr(gate_up[1]), _ptr(down[0]), _ptr(down[1]),
+              _DTYPES[gate_up[1].dtype], group_size, _ptr(offsets), _ptr(out), _ptr(ws),
+              0 if ws is None else ws.numel(), _stream(h.device))
+    return out, offsets
