@@ -1,0 +1,130 @@
+"""pulsarlm-core/tests/kernels/test_marlin.cpp restated against the C++ host layer
+(pulsarlm_amd/_host.so -> C ABI -> HIP): same shape (n=200, k=144, g=16), same
+generators (seeded here), same exactness and allclose(2e-2, 2e-2) checks. Plus the
+linear operator (linear.hpp) with the int4 alternative, on a 3-D input."""
+
+import pytest
+import torch
+
+from pulsarlm_amd import _host
+
+pytestmark = pytest.mark.gpu
+
+N, K, G = 200, 144, 16  # test_marlin.cpp:15-17
+
+
+def cuda(dtype):
+    return dict(device="cuda", dtype=dtype)
+
+
+def random_scale(block_n, gen):  # test_marlin.cpp:23-25
+    return torch.rand(((N + block_n - 1) // block_n, K // G), generator=gen, **cuda(torch.float)) * 0.1 + 0.01
+
+
+def expanded_scale(scale, block_n):  # test_marlin.cpp:27-29
+    return scale.repeat_interleave(block_n, 0)[:N].repeat_interleave(G, 1)
+
+
+def random_fp8(gen):  # test_marlin.cpp:32-36
+    b = torch.randint(0, 256, (N, K), generator=gen, **cuda(torch.uint8))
+    b[(b == 0x7F) | (b == 0xFF)] = 0
+    return b.view(torch.float8_e4m3fn)
+
+
+def random_int4(gen):  # test_marlin.cpp:38-40
+    return torch.randint(-8, 8, (N, K), generator=gen, **cuda(torch.int32))
+
+
+def packed_int4(values):  # test_marlin.cpp:42-46
+    shifts = torch.arange(0, 32, 4, dtype=torch.long)
+    nib = values.cpu().bitwise_and(0xF).to(torch.long).view(N, K // 8, 8)
+    return nib.bitwise_left_shift(shifts).sum(-1).to(torch.int32).cuda()
+
+
+def dequantized(weight, scale, block_n, dtype):  # test_marlin.cpp:48-50
+    return weight.to(dtype) * expanded_scale(scale, block_n).to(dtype)
+
+
+def gen(seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return g
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("block_n", [1, 128])
+def test_fp8_dequantizes_every_e4m3_code_exactly(dtype, block_n):  # test_marlin.cpp:54-65
+    g = gen(1)
+    weight = random_fp8(g)
+    scale = random_scale(block_n, g)
+    wm, sm = _host.repack_fp8_marlin_cuda(weight, scale, block_n, G)
+    identity = torch.eye(K, **cuda(dtype))
+    y = _host.gemm_fp8_marlin_cuda(identity, wm, sm, N, block_n, G)
+    assert torch.equal(y, dequantized(weight, scale, block_n, dtype).t())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("block_n", [1, 128])
+def test_int4_dequantizes_every_int4_value_exactly(dtype, block_n):  # test_marlin.cpp:67-78
+    g = gen(2)
+    values = random_int4(g)
+    scale = random_scale(block_n, g)
+    wm, sm = _host.repack_int4_marlin_cuda(packed_int4(values), scale, block_n, G)
+    identity = torch.eye(K, **cuda(dtype))
+    y = _host.gemm_int4_marlin_cuda(identity, wm, sm, N, block_n, G)
+    assert torch.equal(y, dequantized(values, scale, block_n, dtype).t())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [1, 16, 100])
+def test_fp8_matches_dequantize_then_matmul(dtype, m):  # test_marlin.cpp:80-96
+    g = gen(3 + m)
+    block_n = 128
+    weight = random_fp8(g)
+    scale = random_scale(block_n, g)
+    wm, sm = _host.repack_fp8_marlin_cuda(weight, scale, block_n, G)
+    x = torch.randn((m, K), generator=g, **cuda(dtype))
+    y = _host.gemm_fp8_marlin_cuda(x, wm, sm, N, block_n, G)
+    ref = x.float() @ dequantized(weight, scale, block_n, dtype).float().t()
+    assert torch.allclose(y.float(), ref, 2e-2, 2e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [1, 16, 100])
+def test_int4_matches_dequantize_then_matmul(dtype, m):  # test_marlin.cpp:98-114
+    g = gen(4 + m)
+    block_n = 1
+    values = random_int4(g)
+    scale = random_scale(block_n, g)
+    wm, sm = _host.repack_int4_marlin_cuda(packed_int4(values), scale, block_n, G)
+    x = torch.randn((m, K), generator=g, **cuda(dtype))
+    y = _host.gemm_int4_marlin_cuda(x, wm, sm, N, block_n, G)
+    ref = x.float() @ dequantized(values, scale, block_n, dtype).float().t()
+    assert torch.allclose(y.float(), ref, 2e-2, 2e-2)
+
+
+def test_empty_rows_return_empty_output():  # marlin.cu:573-576
+    g = gen(5)
+    wm, sm = _host.repack_int4_marlin_cuda(packed_int4(random_int4(g)), random_scale(1, g), 1, G)
+    y = _host.gemm_int4_marlin_cuda(torch.empty((0, K), **cuda(torch.bfloat16)), wm, sm, N, 1, G)
+    assert y.shape == (0, N)
+
+
+@pytest.mark.parametrize("kind", ["int4", "fp8"])
+def test_linear_quantized_matches_dense(kind):
+    g = gen(6)
+    if kind == "int4":
+        values = random_int4(g)
+        scale = random_scale(1, g)
+        lin = _host.linear.int4(packed_int4(values), scale, 1, G)
+        dense = dequantized(values, scale, 1, torch.bfloat16)
+    else:
+        weight = random_fp8(g)
+        scale = random_scale(128, g)
+        lin = _host.linear.fp8(weight, scale, 128, G)
+        dense = dequantized(weight, scale, 128, torch.bfloat16)
+    x = torch.randn((3, 5, K), generator=g, **cuda(torch.bfloat16))
+    y = lin.apply(x)
+    assert y.shape == (3, 5, N)
+    ref = _host.linear.dense(dense).apply(x)
+    assert torch.allclose(y.float(), ref.float(), 2e-2, 2e-2)
