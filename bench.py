@@ -5,18 +5,24 @@ Headline (BASELINE.json metric, config 2): W4A16 decode-regime GEMMs at Qwen3-8B
 shapes (qkv 4096->6144, o 4096->4096, gate_up 4096->24576, down 12288->4096),
 int4 g128 symmetric with fp16 scales, bf16 N(0,1) activations, M in {1, 4, 16}.
 A step is one pass over those 12 GEMMs. ``value`` is whole-step algorithmic
-GB/s (weights + scales + x + y bytes / time); inputs are resident in HBM and
+GB/s (weights + scales + x + y bytes / time) with inputs resident in HBM;
 weights rotate over copies totalling > 512 MB so the 256 MB MALL cannot serve
-them. Steps are captured once in a HIP graph and replayed, so host launch cost
-is not measured. Extra fields report the prefill regime (config 3, TFLOP/s vs
-bf16 dense MFMA peak) and config 1.
+them. Launches are captured once in a HIP graph and replayed, so host launch
+cost is not measured (each graph node still costs its dispatch).
+
+Extra objects: the prefill regime (config 3, TFLOP/s vs bf16 dense MFMA peak),
+fp8 block-scaled W8A16 / W8A8 at Qwen3-27B-like shapes (config 4), and the int4
+MoE block at T = 256 / 4096 (config 5).
 
 ``roofline`` covers the dominant kernel (the decode kernel): achieved =
 algorithmic bytes per launch / average launch time from HIP events around the
-graph replays on the launch stream. ``cpu_baseline`` times the oracle's
-dequantize-then-matmul (numpy, all host cores) on config 1.
+graph replays on the launch stream; ``traffic`` comes from the committed
+rocprofv3 FETCH_SIZE/WRITE_SIZE measurement (profiles/decode_traffic.json) when
+present. ``cpu_baseline`` times the oracle's dequantize-then-matmul (numpy, all
+host cores) on config 1.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+       [--only decode|prefill|fp8|moe] [--eager] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -29,13 +35,17 @@ import time
 
 import numpy as np
 
+ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP8_PEAK_TFLOPS = 5000.0
+MALL_BYTES = 600_000_000  # rotate over more than this (the Infinity Cache is 256 MB)
 
 SHAPES = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 24576), ("down", 12288, 4096)]
+FP8_SHAPES = [("qkv", 5120, 7168), ("o", 5120, 5120), ("gate_up", 5120, 34816), ("down", 17408, 5120)]
 DECODE_M = [1, 4, 16]
 PREFILL_M = [256, 1024, 4096]
+FP8_M = [1, 16, 2048]
 GROUP = 128
 
 
@@ -43,30 +53,20 @@ def w4a16_bytes(m, n, k, g=GROUP):
     return n * k // 2 + n * (k // g) * 2 + m * k * 2 + m * n * 2
 
 
+def fp8_bytes(m, n, k, a8=False):
+    return n * k + (n // 128) * (k // 128) * 4 + m * k * (1 if a8 else 2) + m * n * 2
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--quick", action="store_true", help="skip the prefill sweep and the CPU baseline")
+    p.add_argument("--steps", type=int, default=24)
+    p.add_argument("--warmup", type=int, default=6)
+    p.add_argument("--quick", action="store_true", help="decode headline only")
+    p.add_argument("--only", choices=["decode", "prefill", "fp8", "moe", "copy"], default=None)
+    p.add_argument("--eager", action="store_true", help="no graphs (for profiler attribution)")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
-
-
-class Layer:
-    """One repacked int4 weight (several rotating copies) for a K->N shape."""
-
-    def __init__(self, torch, ops, k, n, copies, seed):
-        from oracle import oracle as O  # seeded synthetic inputs only
-        _, packed, scale = O.make_w4a16(1, n, k, GROUP, seed=seed)
-        pk = torch.from_numpy(packed).cuda()
-        sc = torch.from_numpy(scale).cuda()
-        w, s = ops.repack_int4_marlin_cuda(pk, sc, 1, GROUP)
-        # Enough copies that rotating over them alone exceeds 512 MB (the MALL is 256 MB).
-        copies = max(copies, -(-600_000_000 // (w.numel() * 4 + s.numel() * 2)))
-        self.copies = [(w, s)] + [(w.clone(), s.clone()) for _ in range(copies - 1)]
-        self.k, self.n = k, n
-        del pk, sc
 
 
 def cpu_baseline(budget_s=15.0):
@@ -90,174 +90,274 @@ def cpu_baseline(budget_s=15.0):
             break
     med = float(np.median(times))
     return {
-        "value": w4a16_bytes(16, 4096, 4096) / med / 1e9,
+        "value": round(w4a16_bytes(16, 4096, 4096) / med / 1e9, 4),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
         "sample": f"config 1 (M=16, K=N=4096, int4 g128) x{len(times)} runs, median "
                   f"{med * 1e3:.1f} ms (dequant {np.median(tdq) * 1e3:.1f} ms, matmul {np.median(tmm) * 1e3:.1f} ms), "
-                  f"numpy oracle",
+                  f"numpy oracle, BLAS threads = host cores",
     }
+
+
+class Bench:
+    def __init__(self, eager: bool):
+        import torch
+
+        from pulsarlm_amd import _lib, ops
+
+        self.torch, self.lib, self.ops, self._lib = torch, _lib.load(), ops, _lib
+        self.dev = torch.device("cuda:0")
+        self.stream = torch.cuda.Stream()
+        self.ws = torch.zeros(256 << 20, dtype=torch.uint8, device=self.dev)
+        self.eager = eager
+
+    def time(self, launches, reps=5, warm=1):
+        """Seconds per pass over `launches` (callables enqueuing on self.stream)."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for f in launches:  # eager warm-up (first-call setup happens here)
+                f()
+            self.stream.synchronize()
+            if self.eager:
+                run = lambda: [f() for f in launches]  # noqa: E731
+            else:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=self.stream):
+                    for f in launches:
+                        f()
+                run = g.replay
+            for _ in range(warm):
+                run()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(self.stream)
+            for _ in range(reps):
+                run()
+            e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / reps
+
+    def int4_layer(self, k, n, seed, min_copies=1):
+        from oracle import oracle as O  # seeded synthetic inputs only
+        torch = self.torch
+        _, packed, scale = O.make_w4a16(1, n, k, GROUP, seed=seed)
+        w, s = self.ops.repack_int4_marlin_cuda(torch.from_numpy(packed).to(self.dev),
+                                                torch.from_numpy(scale).to(self.dev), 1, GROUP)
+        nc = max(min_copies, -(-MALL_BYTES // (w.numel() * 4 + s.numel() * 2)))
+        return [(w, s)] + [(w.clone(), s.clone()) for _ in range(nc - 1)]
+
+    def gemm_launch(self, fmt, x, w, s, sdt, m, n, k, bn, y, a8=False):
+        lib, L, st = self.lib, self._lib, self.stream.cuda_stream
+        ws, wsn = self.ws.data_ptr(), self.ws.numel()
+        xd = L.PLM_BF16
+        if a8:
+            return lambda: L.check(lib.plm_gemm_w8a8(x.data_ptr(), xd, w.data_ptr(), s.data_ptr(), sdt, m, n, k, bn,
+                                                     GROUP, y.data_ptr(), ws, wsn, st))
+        return lambda: L.check(lib.plm_gemm(fmt, x.data_ptr(), xd, w.data_ptr(), s.data_ptr(), sdt, m, n, k, bn,
+                                            GROUP, y.data_ptr(), ws, wsn, st))
+
+
+def section_decode(b: Bench, steps, warmup):
+    torch, L = b.torch, b._lib
+    layers = {name: b.int4_layer(k, n, i, min_copies=6) for i, (name, k, n) in enumerate(SHAPES)}
+    xs = {(m, k): torch.randn(m, k, device=b.dev).to(torch.bfloat16) for m in DECODE_M for k in (4096, 12288)}
+    ys = {(m, n): torch.empty(m, n, device=b.dev, dtype=torch.bfloat16) for m in DECODE_M for (_, _, n) in SHAPES}
+
+    def launches_for(names, ms, copies):
+        out = []
+        for c in range(copies):
+            for name, k, n in SHAPES:
+                if name not in names:
+                    continue
+                w, s = layers[name][c % len(layers[name])]
+                for m in ms:
+                    out.append(b.gemm_launch(L.PLM_INT4, xs[(m, k)], w, s, L.PLM_FP16, m, n, k, 1, ys[(m, n)]))
+        return out
+
+    # Headline: the 12-GEMM step, rotated over 6 copies of the layer set (~600 MB).
+    copies = 6
+    reps = max(1, -(-steps // copies))
+    t_pass = b.time(launches_for({s[0] for s in SHAPES}, DECODE_M, copies), reps=reps, warm=max(1, warmup // copies))
+    step_bytes = sum(w4a16_bytes(m, n, k) for (_, k, n) in SHAPES for m in DECODE_M)
+    t_step = t_pass / copies
+    detail = {}
+    for name, k, n in SHAPES:
+        for m in DECODE_M:
+            nc = len(layers[name])
+            tt = b.time(launches_for({name}, [m], nc), reps=5) / nc
+            gbs = w4a16_bytes(m, n, k) / tt / 1e9
+            detail[f"{name}_m{m}"] = {"us": round(tt * 1e6, 2), "GB/s": round(gbs, 1),
+                                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 3)}
+    launches_per_step = len(SHAPES) * len(DECODE_M)
+    return {
+        "value": step_bytes / t_step / 1e9,
+        "steps": reps * copies,
+        "warmup": max(1, warmup // copies) * copies,
+        "ms_per_step": t_step * 1e3,
+        "per_launch_bytes": step_bytes / launches_per_step,
+        "avg_launch_s": t_step / launches_per_step,
+        "detail": detail,
+    }
+
+
+def section_prefill(b: Bench):
+    torch, L = b.torch, b._lib
+    out = {}
+    tot_flop = tot_t = 0.0
+    for i, (name, k, n) in enumerate(SHAPES):
+        copies = b.int4_layer(k, n, i, min_copies=2)
+        for m in PREFILL_M:
+            x = torch.randn(m, k, device=b.dev).to(torch.bfloat16)
+            y = torch.empty(m, n, device=b.dev, dtype=torch.bfloat16)
+            launches = [b.gemm_launch(L.PLM_INT4, x, w, s, L.PLM_FP16, m, n, k, 1, y) for (w, s) in copies]
+            tt = b.time(launches, reps=2 if m == 4096 else 4) / len(copies)
+            tf = 2 * m * n * k / tt / 1e12
+            tot_flop += 2 * m * n * k
+            tot_t += tt
+            out[f"{name}_m{m}"] = {"us": round(tt * 1e6, 1), "TFLOP/s": round(tf, 1),
+                                   "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 3)}
+        del copies
+    out["aggregate_TFLOP/s"] = round(tot_flop / tot_t / 1e12, 1)
+    return out
+
+
+def section_fp8(b: Bench):
+    from oracle import oracle as O
+    torch, L, ops = b.torch, b._lib, b.ops
+    out = {}
+    for i, (name, k, n) in enumerate(FP8_SHAPES):
+        rng = np.random.default_rng(40 + i)
+        w = O.bf16_round(rng.standard_normal((n, k), dtype=np.float32) * 0.02)
+        codes, scale = O.fp8_block_quantize(w, 128, 128)
+        wt, st = ops.repack_fp8_marlin_cuda(torch.from_numpy(codes).to(b.dev).view(torch.float8_e4m3fn),
+                                            torch.from_numpy(scale).to(b.dev), 128, 128)
+        nc = max(2, -(-MALL_BYTES // (wt.numel() * 4)))
+        copies = [(wt, st)] + [(wt.clone(), st.clone()) for _ in range(nc - 1)]
+        for m in FP8_M:
+            x = torch.randn(m, k, device=b.dev).to(torch.bfloat16)
+            y = torch.empty(m, n, device=b.dev, dtype=torch.bfloat16)
+            for a8 in (False, True):
+                launches = [b.gemm_launch(L.PLM_FP8, x, w_, s_, L.PLM_FP32, m, n, k, 128, y, a8=a8)
+                            for (w_, s_) in copies]
+                tt = b.time(launches, reps=3) / len(copies)
+                key = f"{name}_m{m}_{'w8a8' if a8 else 'w8a16'}"
+                gbs = fp8_bytes(m, n, k, a8) / tt / 1e9
+                tf = 2 * m * n * k / tt / 1e12
+                peak = FP8_PEAK_TFLOPS if a8 else BF16_PEAK_TFLOPS
+                out[key] = {"us": round(tt * 1e6, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3),
+                            "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / peak, 3)}
+        del copies
+    return out
+
+
+def section_moe(b: Bench):
+    from oracle import oracle as O
+    torch, ops = b.torch, b.ops
+    e, hidden, inter, top_k = 128, 2048, 768, 8
+    rng = np.random.default_rng(5)
+
+    def experts(n, k):
+        packed = rng.integers(-2**31, 2**31, size=(e, n, k // 8), dtype=np.int64).astype(np.int32)
+        scale = (np.abs(rng.standard_normal((e, n, k // GROUP)) * 0.02) + 1e-3).astype(np.float16)
+        return ops.repack_int4_experts(torch.from_numpy(packed).to(b.dev), torch.from_numpy(scale).to(b.dev), GROUP)
+
+    gu, dn = experts(2 * inter, hidden), experts(hidden, inter)
+    out = {}
+    for t in (256, 4096):
+        ex, wts = O.zipf_routing(t, e, top_k, seed=t)
+        h = torch.randn(t, hidden, device=b.dev).to(torch.bfloat16)
+        te = torch.from_numpy(ex.astype(np.int32)).to(b.dev)
+        tw = torch.from_numpy(wts).to(b.dev)
+        hit = len(np.unique(ex))
+        tt = b.time([lambda: ops.routed_experts_int4_cuda(h, te, tw, gu, dn, inter, GROUP)], reps=5)
+        rows = t * top_k
+        flop = 2 * rows * (hidden * 2 * inter + inter * hidden)
+        wbytes = hit * (2 * inter * hidden // 2 + 2 * inter * (hidden // GROUP) * 2 + hidden * inter // 2 +
+                        hidden * (inter // GROUP) * 2)
+        act_bytes = rows * hidden * 2 + rows * 2 * inter * 2 * 2 + rows * inter * 2 * 2 + rows * hidden * 2 * 2
+        out[f"T{t}"] = {"us": round(tt * 1e6, 1), "experts_hit": hit,
+                        "GB/s": round((wbytes + act_bytes) / tt / 1e9, 1),
+                        "frac_hbm": round((wbytes + act_bytes) / tt / 1e9 / HBM_PEAK_GBS, 3),
+                        "TFLOP/s": round(flop / tt / 1e12, 1),
+                        "frac_mfma": round(flop / tt / 1e12 / BF16_PEAK_TFLOPS, 3)}
+    return out
+
+
+def section_copy(b: Bench):
+    """A plain device copy of known size: the calibration run for the FETCH_SIZE /
+    WRITE_SIZE counters (their reading for 256 MiB read + 256 MiB written)."""
+    torch = b.torch
+    nbytes = 256 << 20
+    src = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=b.dev)
+    dst = torch.empty_like(src)
+    tt = b.time([lambda: dst.copy_(src)], reps=5)
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": round(tt * 1e6, 1),
+            "GB/s": round(2 * nbytes / tt / 1e9, 1)}
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(no multi-GPU path: the north star is single-GPU)", file=sys.stderr)
+              "(the hot path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
-
+    sys.path.insert(0, ROOT)
     import torch
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from pulsarlm_amd import _lib, ops
 
     torch.cuda.init()
-    dev = torch.device("cuda:0")
     torch.manual_seed(0)
-    lib = _lib.load()
+    b = Bench(args.eager)
+    if args.only and args.only != "decode":
+        fn = {"prefill": section_prefill, "fp8": section_fp8, "moe": section_moe, "copy": section_copy}[args.only]
+        print(json.dumps({args.only: fn(b)}))
+        return
 
-    # Rotating weight copies: 99.4 MB per layer set -> 6 copies ~ 600 MB > 512 MB.
-    copies = 6
-    layers = [Layer(torch, ops, k, n, copies, seed=i) for i, (_, k, n) in enumerate(SHAPES)]
-    xs = {m: {k: torch.randn(m, k, device=dev).to(torch.bfloat16) for k in (4096, 12288)}
-          for m in DECODE_M + PREFILL_M}
-    ys = {(m, n): torch.empty(m, n, device=dev, dtype=torch.bfloat16) for m in DECODE_M + PREFILL_M
-          for n in (4096, 6144, 24576)}
-    ws_bytes = max(lib.plm_gemm_workspace_bytes(_lib.PLM_INT4, m, n, k)
-                   for m in DECODE_M + PREFILL_M for (_, k, n) in SHAPES)
-    ws = torch.zeros(max(ws_bytes, 1 << 16), dtype=torch.uint8, device=dev)
-    stream = torch.cuda.Stream()
-
-    def launch(m, layer, copy):
-        w, s = layer.copies[copy]
-        x = xs[m][layer.k]
-        y = ys[(m, layer.n)]
-        rc = lib.plm_gemm(_lib.PLM_INT4, x.data_ptr(), _lib.PLM_BF16, w.data_ptr(), s.data_ptr(), _lib.PLM_FP16,
-                          m, layer.n, layer.k, 1, GROUP, y.data_ptr(), ws.data_ptr(), ws.numel(),
-                          stream.cuda_stream)
-        _lib.check(rc)
-
-    def capture(ms):
-        """One graph = every copy x every layer x every M in ms (rotation inside the graph)."""
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(stream):
-            for c in range(copies):  # eager warm-up of every launch
-                for L in layers:
-                    for m in ms:
-                        launch(m, L, c)
-            stream.synchronize()
-            with torch.cuda.graph(g, stream=stream):
-                for c in range(copies):
-                    for L in layers:
-                        for m in ms:
-                            launch(m, L, c)
-        return g
-
-    def time_graph(g, reps, warm):
-        # Replays run on `stream` (the stream the kernels were captured on), and the
-        # events bracketing them are recorded on the same stream.
-        with torch.cuda.stream(stream):
-            for _ in range(warm):
-                g.replay()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(reps):
-                g.replay()
-            e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / 1e3  # seconds
-
-    # ---------------- decode regime (headline) ----------------
-    g_dec = capture(DECODE_M)
-    # A step = the 12 GEMMs; one graph replay = `copies` steps.
-    reps = max(1, -(-args.steps // copies))
-    warm = max(1, -(-args.warmup // copies))
-    t = time_graph(g_dec, reps, warm)
-    steps = reps * copies
-    step_bytes = sum(w4a16_bytes(m, n, k) for (_, k, n) in SHAPES for m in DECODE_M)
-    ms_per_step = t / steps * 1e3
-    value = step_bytes * steps / t / 1e9
-    launches = steps * len(SHAPES) * len(DECODE_M)
-    per_launch_bytes = step_bytes / (len(SHAPES) * len(DECODE_M))
-    avg_launch_s = t / launches
-
-    # Per-shape / per-M breakdown (each its own graph, same rotation).
-    detail = {}
-    for name, k, n in SHAPES:
-        L = layers[[s[0] for s in SHAPES].index(name)]
-        for m in DECODE_M:
-            g = torch.cuda.CUDAGraph()
-            nc = len(L.copies)
-            with torch.cuda.stream(stream):
-                for c in range(nc):
-                    launch(m, L, c)
-                stream.synchronize()
-                with torch.cuda.graph(g, stream=stream):
-                    for c in range(nc):
-                        launch(m, L, c)
-            tt = time_graph(g, 10, 1) / (10 * nc)
-            detail[f"{name}_m{m}"] = {"us": round(tt * 1e6, 2),
-                                      "GB/s": round(w4a16_bytes(m, n, k) / tt / 1e9, 1),
-                                      "frac_hbm": round(w4a16_bytes(m, n, k) / tt / 1e9 / HBM_PEAK_GBS, 3)}
-
-    # ---------------- prefill regime (config 3) ----------------
-    prefill = {}
-    if not args.quick:
-        for name, k, n in SHAPES:
-            L = layers[[s[0] for s in SHAPES].index(name)]
-            for m in PREFILL_M:
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.stream(stream):
-                    launch(m, L, 0)
-                    stream.synchronize()
-                    with torch.cuda.graph(g, stream=stream):
-                        for c in range(copies):
-                            launch(m, L, c)
-                reps_p = 3 if m == 4096 else 5
-                tt = time_graph(g, reps_p, 1) / (reps_p * copies)
-                tf = 2 * m * n * k / tt / 1e12
-                prefill[f"{name}_m{m}"] = {"us": round(tt * 1e6, 1), "TFLOP/s": round(tf, 1),
-                                           "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 3)}
-        tot_flop = sum(2 * m * n * k for (_, k, n) in SHAPES for m in PREFILL_M)
-        tot_t = sum(v["us"] for v in prefill.values()) * 1e-6
-        prefill["aggregate_TFLOP/s"] = round(tot_flop / tot_t / 1e12, 1)
-
+    d = section_decode(b, args.steps, args.warmup)
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    achieved = d["per_launch_bytes"] / d["avg_launch_s"] / 1e9
     result = {
         "metric": "W4A16 GEMM GB/s & TFLOP/s (% roofline) at M=1..4096, Qwen3-8B shapes",
-        "value": round(value, 1),
+        "value": round(d["value"], 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": warm * copies,
-        "ms_per_step": round(ms_per_step, 4),
+        "steps": d["steps"],
+        "warmup": d["warmup"],
+        "ms_per_step": round(d["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4 weights x bf16 activations, fp32 accumulate",
         "data": "synthetic (seeded: x ~ N(0,1) bf16, q ~ U[-8,7], fp16 scales |N(0,.02)|+1e-3)",
         "config": {
-            "workload": "BASELINE config 2: Qwen3-8B decode layer set (qkv, o, gate_up, down) x M in {1,4,16}, "
-                        "int4 g128, one step = 12 GEMMs, weights rotated over 6 copies (~600 MB)",
-            "shapes_KxN": [[k, n] for (_, k, n) in SHAPES],
+            "workload": "BASELINE config 2: Qwen3-8B decode layer set (qkv 4096->6144, o 4096->4096, gate_up "
+                        "4096->24576, down 12288->4096) x M in {1,4,16}, int4 g128; one step = 12 GEMMs; weights "
+                        "rotated over 6 copies (~600 MB) so the 256 MB MALL cannot serve them",
             "M": DECODE_M,
             "group_size": GROUP,
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(per_launch_bytes / avg_launch_s / 1e9, 1),
+            "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(per_launch_bytes / avg_launch_s / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "decode_kernel (plm_gemm, M<=16)",
-            "algorithmic_bytes_per_launch": int(per_launch_bytes),
-            "avg_launch_us": round(avg_launch_s * 1e6, 3),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "decode_kernel (plm_gemm, M <= 16)",
+            "algorithmic_bytes_per_launch": int(d["per_launch_bytes"]),
+            "avg_launch_us": round(d["avg_launch_s"] * 1e6, 3),
         },
-        "decode_detail": detail,
-        "prefill_config3": prefill,
+        "decode_detail": d["detail"],
     }
-    if not args.quick and not args.no_cpu:
+    if not args.quick and args.only is None:
+        result["prefill_config3"] = section_prefill(b)
+        result["fp8_config4"] = section_fp8(b)
+        result["moe_config5"] = section_moe(b)
+    if not args.quick and not args.no_cpu and args.only is None:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result))
 
