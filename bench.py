@@ -66,6 +66,7 @@ def parse():
     p.add_argument("--only", choices=["decode", "prefill", "fp8", "moe", "copy"], default=None)
     p.add_argument("--eager", action="store_true", help="no graphs (for profiler attribution)")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-detail", action="store_true", help="headline step only (profiler runs)")
     return p.parse_args()
 
 
@@ -158,7 +159,7 @@ class Bench:
                                             GROUP, y.data_ptr(), ws, wsn, st))
 
 
-def section_decode(b: Bench, steps, warmup):
+def section_decode(b: Bench, steps, warmup, detail_shapes=True):
     torch, L = b.torch, b._lib
     layers = {name: b.int4_layer(k, n, i, min_copies=6) for i, (name, k, n) in enumerate(SHAPES)}
     xs = {(m, k): torch.randn(m, k, device=b.dev).to(torch.bfloat16) for m in DECODE_M for k in (4096, 12288)}
@@ -182,7 +183,7 @@ def section_decode(b: Bench, steps, warmup):
     step_bytes = sum(w4a16_bytes(m, n, k) for (_, k, n) in SHAPES for m in DECODE_M)
     t_step = t_pass / copies
     detail = {}
-    for name, k, n in SHAPES:
+    for name, k, n in (SHAPES if detail_shapes else []):
         for m in DECODE_M:
             nc = len(layers[name])
             tt = b.time(launches_for({name}, [m], nc), reps=5) / nc
@@ -313,7 +314,7 @@ def main():
         print(json.dumps({args.only: fn(b)}))
         return
 
-    d = section_decode(b, args.steps, args.warmup)
+    d = section_decode(b, args.steps, args.warmup, detail_shapes=not args.no_detail)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "decode_traffic.json")
     if os.path.exists(tpath):
