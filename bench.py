@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X quantized-linear hot path (one GPU).
 
-Headline (BASELINE.json metric, config 2): W4A16 decode-regime GEMMs at Qwen3-8B
+Headline (headline metric, config 2): W4A16 decode-regime GEMMs at Qwen3-8B
 shapes (qkv 4096->6144, o 4096->4096, gate_up 4096->24576, down 12288->4096),
 int4 g128 symmetric with fp16 scales, bf16 N(0,1) activations, M in {1, 4, 16}.
 A step is one pass over those 12 GEMMs. ``value`` is whole-step algorithmic
@@ -301,7 +301,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the hot path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the hot path is single-GPU)", file=sys.stderr)
         sys.exit(2)
     sys.path.insert(0, ROOT)
     import torch
@@ -335,7 +335,7 @@ def main():
         "dtype": "int4 weights x bf16 activations, fp32 accumulate",
         "data": "synthetic (seeded: x ~ N(0,1) bf16, q ~ U[-8,7], fp16 scales |N(0,.02)|+1e-3)",
         "config": {
-            "workload": "BASELINE config 2: Qwen3-8B decode layer set (qkv 4096->6144, o 4096->4096, gate_up "
+            "workload": "benchmark config 2: Qwen3-8B decode layer set (qkv 4096->6144, o 4096->4096, gate_up "
                         "4096->24576, down 12288->4096) x M in {1,4,16}, int4 g128; one step = 12 GEMMs; weights "
                         "rotated over 6 copies (~600 MB) so the 256 MB MALL cannot serve them",
             "M": DECODE_M,

@@ -421,7 +421,7 @@ def sparse_moe_ref(h, top_experts, top_weights, gate_up, down, dtype="bf16"):
 
 
 # ---------------------------------------------------------------------------
-# Seeded synthetic inputs
+# Seeded synthetic inputs (benchmark configs)
 # ---------------------------------------------------------------------------
 
 

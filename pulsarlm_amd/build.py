@@ -31,7 +31,7 @@ FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
-    # Packed fp32 VALU ops are kept out of generated code (see DESIGN: packed-fp32).
+    # Packed fp32 VALU ops (v_pk_*_f32) are kept out of generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{PKG.parent / 'include'}",
 ]

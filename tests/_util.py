@@ -23,7 +23,7 @@ def to_np(t: torch.Tensor) -> np.ndarray:
 
 
 def int4_case(n, k, g, block_n=1, seed=0, scale_dtype=np.float16, scale_kind="baseline"):
-    """q uniform [-8, 7] packed LSB-first, scales per BASELINE (|N(0,.02)|+1e-3) or the
+    """q uniform [-8, 7] packed LSB-first, scales per the benchmark spec (|N(0,.02)|+1e-3) or the
     reference test's rand*0.1+0.01 (test_marlin.cpp:23-25)."""
     rng = np.random.default_rng(seed)
     q = rng.integers(-8, 8, size=(n, k))

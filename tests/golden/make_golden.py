@@ -3,7 +3,7 @@
 The reference commits no golden vectors for this path (its tests draw unseeded
 random tensors on the device, pulsarlm-core/tests/kernels/test_marlin.cpp), so
 these fixtures are seeded inputs with the oracle's expected outputs at the
-reference test's shape (n=200, k=144, g=16) and a slice of BASELINE config 1.
+reference test's shape (n=200, k=144, g=16) and a slice of benchmark config 1.
 They pin the oracle and the GPU path against regressions.
 
     python tests/golden/make_golden.py

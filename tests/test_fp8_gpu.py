@@ -1,6 +1,6 @@
 """fp8 paths on the GPU: per-row e4m3 activation quantization (bit-exact vs the
 oracle) and the W8A8 GEMM (tolerance vs the oracle's exact-product reference),
-plus W8A16 at the BASELINE config-4 shapes. The W8A8 mode has no reference
+plus W8A16 at the benchmark config-4 shapes. The W8A8 mode has no reference
 counterpart: its parity is pinned only by the oracle restatement."""
 
 import numpy as np
@@ -49,7 +49,7 @@ def test_w8a8_matches_oracle(m, dtype):
 @pytest.mark.parametrize("shape", [(5120, 7168), (5120, 5120), (5120, 34816), (17408, 5120)])
 @pytest.mark.parametrize("m", [1, 16, 2048])
 def test_config4_qwen3_27b_shapes(shape, m):
-    """fp8 128x128 block weights, W8A16 (bf16 x) and W8A8."""
+    """benchmark config 4: fp8 128x128 block weights, W8A16 (bf16 x) and W8A8."""
     k, n = shape
     codes, scale, wt, st = _fp8_weights(n, k, seed=k + n)
     x = O.bf16_round(np.random.default_rng(m).standard_normal((m, k)).astype(np.float32))

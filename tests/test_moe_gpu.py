@@ -77,7 +77,7 @@ def test_routed_experts_matches_oracle(t, e, hidden, inter, top_k):
 
 
 def test_config5_t4096_sample():
-    """BASELINE config 5 at T=4096 (E=128, top-8, H=2048, I=768); the CPU oracle
+    """benchmark config 5 at T=4096 (E=128, top-8, H=2048, I=768); the CPU oracle
     checks a sample of 64 tokens (full-size parity via the same kernels at T=256)."""
     t, e, hidden, inter, top_k, g = 4096, 128, 2048, 768, 8, 128
     h, experts, weights, gu, dn = _moe_case(t, e, hidden, inter, top_k, g, seed=5)
