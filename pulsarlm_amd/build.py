@@ -37,9 +37,15 @@ FLAGS = [
 ]
 
 
+# Per-source flags. The MFMA kernel keeps its accumulators in VGPRs (the VGPR form of
+# v_mfma): with the default AGPR form the register allocator splits the accumulator set
+# between the two files and copies it back and forth every K step.
+SOURCE_FLAGS = {"gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")

@@ -14,8 +14,11 @@
 //   SIMD with the full 512 registers), so each dequantized weight feeds 8 MFMAs and the
 //   dequant VALU work is about half the MFMA time, interleaved with it.
 // * The x tile and the packed weight tiles (1 KiB int4 / 2 KiB fp8 per 16-column strip,
-//   copied verbatim from the plm layout) are staged through LDS; the next K step's global
-//   loads are in flight in registers during the current step's MFMAs.
+//   copied verbatim from the plm layout) go from HBM straight into LDS with buffer loads to
+//   LDS (no register staging), double-buffered: the next K step's loads land in one stage
+//   while the current step's MFMAs read the other, with one barrier per K step. x rows are
+//   XOR-swizzled in LDS so that fragment reads are free of bank conflicts; rows past M and
+//   columns past K read as zeros through the buffer range instead of branches.
 // * Weights are dequantized in registers to round(q * round(s)), bit-identical to the
 //   reference's fragment values (shared dq_int4 / dq_fp8).
 // * A8 (W8A8): x is e4m3 (quantized per row beforehand) and every 128-wide K tile is one
@@ -58,28 +61,35 @@ struct mfma_args {
 namespace {
 
 template <bool A8> struct a_traits {
-    static constexpr int row_bytes = A8 ? kTileK : kTileK * 2;
-    static constexpr int lds_row = row_bytes + 16;  // padded LDS row
+    static constexpr int row_bytes = A8 ? kTileK : kTileK * 2;  // one A row of one K tile
+    static constexpr int slots = row_bytes / 16;                 // its 16-byte slots
 };
 
-template <plm_format F, bool BF16, bool UNIFORM, bool A8, bool GROUPED, int WM, int WN, int MT, int NS>
+template <plm_format F, bool BF16, bool UNIFORM, bool WIDE, bool A8, bool GROUPED, int WM, int WN, int MT, int NS>
 __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
-    constexpr int NT = WM * WN * 64;  // threads
+    constexpr int NW = WM * WN;  // wavefronts
+    constexpr int NT = NW * 64;
     constexpr int TB = fmt_traits<F>::tile_bytes;
     constexpr int BM = WM * MT * 16;
     constexpr int BS = WN * NS;  // strips per workgroup
     constexpr int ARB = a_traits<A8>::row_bytes;
-    constexpr int ALR = a_traits<A8>::lds_row;
-    constexpr int A_BYTES = BM * ALR;
-    constexpr int B_BYTES = BS * TB;
-    constexpr int A_CHUNKS = BM * ARB / 16;
-    constexpr int B_CHUNKS = B_BYTES / 16;
-    constexpr int A_LOADS = (A_CHUNKS + NT - 1) / NT;
-    constexpr int B_LOADS = (B_CHUNKS + NT - 1) / NT;
-    constexpr int CPR = ARB / 16;  // 16-byte chunks per A row
+    constexpr int SLOTS = a_traits<A8>::slots;
+    constexpr int RPC = 1024 / ARB;  // A rows per 1 KiB chunk
+    constexpr int A_STAGE = BM * ARB;
+    constexpr int B_STAGE = BS * TB;
+    constexpr int STAGE = A_STAGE + B_STAGE;
+    constexpr int A_PW = A_STAGE / 1024 / NW;  // 1 KiB chunks each wavefront loads per K step
+    constexpr int B_PW = B_STAGE / 1024 / NW;
+    static_assert(A_STAGE % (1024 * NW) == 0 && B_STAGE % (1024 * NW) == 0, "chunks split evenly over wavefronts");
+    constexpr int ST = UNIFORM ? 1 : 4;  // scale values per strip per K step
+    constexpr int ES = WIDE ? 4 : 2;     // scale element bytes
 
-    __shared__ __attribute__((aligned(16))) uint8_t lds[A_BYTES + B_BYTES];
-    __shared__ uint32_t last_flag;
+    // Two stages of [A tile | weight tiles]. Stage s holds K step kt_begin + s (mod 2); the
+    // loads of step kt + 1 go straight from HBM into the other stage while step kt computes.
+    // The split-K arrival flag reuses the first word once the K loop is over (arrive_last
+    // synchronizes the workgroup before writing it).
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+    uint32_t& last_flag = *reinterpret_cast<uint32_t*>(lds);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -109,111 +119,130 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     const uint8_t* wbase = a.w + (GROUPED ? expert * a.w_expert_bytes : 0);
     const void* sbase = static_cast<const uint8_t*>(a.scale) + (GROUPED ? expert * a.s_expert_bytes : 0);
 
+    // A source: row-major rows of ARB bytes per K tile. Plain calls address rows from row0 and
+    // bound the buffer at `rows` rows; grouped calls gather rows through row_index (the host
+    // checks every offset stays below kOOB).
+    const int a_stride = A8 ? a.ktiles * kTileK : a.k * 2;
+    __amdgpu_buffer_rsrc_t a_rsrc;
+    if constexpr (GROUPED) {
+        a_rsrc = make_rsrc(a.x, static_cast<uint32_t>(kOOB));
+    } else {
+        const uint8_t* base = A8 ? a.xq : reinterpret_cast<const uint8_t*>(a.x);
+        a_rsrc = make_rsrc(base + static_cast<int64_t>(row0) * a_stride, static_cast<uint32_t>(rows * a_stride));
+    }
+    // Chunk c of the A tile is rows c*RPC .. c*RPC+RPC-1; lane L of its load writes slot L % SLOTS
+    // of row c*RPC + L / SLOTS, which holds the row's 16-byte column (slot ^ row % SLOTS): the XOR
+    // swizzle puts the 16 rows of one MFMA fragment read in 16 different bank groups.
+    int a_off[A_PW], a_col[A_PW];
+#pragma unroll
+    for (int i = 0; i < A_PW; ++i) {
+        const int r = (wave * A_PW + i) * RPC + lane / SLOTS;
+        const int c = (lane % SLOTS) ^ (r % SLOTS);
+        int src = -1;
+        if (r < rows) {
+            if constexpr (GROUPED) src = a.row_index != nullptr ? a.row_index[row0 + r] : row0 + r;
+            else src = r;
+        }
+        a_off[i] = src < 0 ? kOOB : src * a_stride + c * 16;
+        a_col[i] = c * 8;  // bf16 elements into the K tile (tail check, bf16 only)
+    }
+    // Weights: this workgroup's strips are contiguous, ktiles * TB bytes each.
+    const int strip_bytes = a.ktiles * TB;
+    const __amdgpu_buffer_rsrc_t b_rsrc =
+        make_rsrc(wbase + static_cast<int64_t>(strip0) * strip_bytes,
+                  static_cast<uint32_t>(min(BS, a.strips - strip0) * strip_bytes));
+    int b_off[B_PW];
+#pragma unroll
+    for (int i = 0; i < B_PW; ++i) {
+        const int c = wave * B_PW + i;
+        b_off[i] = (c / (TB / 1024)) * strip_bytes + (c % (TB / 1024)) * 1024 + lane * 16;
+    }
+
+    auto issue = [&](int kt, int stage) {
+        uint8_t* sa = lds + stage * STAGE;
+#pragma unroll
+        for (int i = 0; i < A_PW; ++i) {
+            int off = a_off[i];
+            if constexpr (!UNIFORM) {
+                if (kt * kTileK + a_col[i] >= a.k) off = kOOB;
+            }
+            buffer_load_lds16(a_rsrc, sa + (wave * A_PW + i) * 1024, off, kt * ARB);
+        }
+#pragma unroll
+        for (int i = 0; i < B_PW; ++i)
+            buffer_load_lds16(b_rsrc, sa + A_STAGE + (wave * B_PW + i) * 1024, b_off[i], kt * TB);
+    };
+
+    // Scales of this workgroup's strips ([strip][group][scale_cols], ES bytes each), loaded as
+    // raw bits one K step ahead and converted when used, so that no wait on them stalls the
+    // tile loads in flight. Strips past N read as zero.
+    const bool bf16_scale = a.scale_dtype == PLM_BF16;
+    const int s_row = a.groups * a.scale_cols * ES;  // bytes per strip
+    const __amdgpu_buffer_rsrc_t s_rsrc =
+        make_rsrc(static_cast<const uint8_t*>(sbase) + static_cast<int64_t>(strip0) * s_row,
+                  static_cast<uint32_t>(min(BS, a.strips - strip0) * s_row));
+    const int s_lane = (a.scale_cols == 1 ? 0 : col16 * ES) + wn * NS * s_row;
+    auto scale_bits = [&](int j, int kt, int t) -> uint32_t {
+        int voff = s_lane + j * s_row, soff = 0;
+        if constexpr (UNIFORM) soff = uniform(kt * kTileK / a.group_size) * a.scale_cols * ES;
+        else voff += (kt * kTileK + 32 * t + 8 * kq) / a.group_size * a.scale_cols * ES;
+        if constexpr (WIDE) return buffer_load_u32(s_rsrc, voff, soff);
+        else return buffer_load_u16(s_rsrc, voff, soff);
+    };
+
     f32x4_t acc[MT][NS];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < NS; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // Source row of A chunk c: row0 + c / CPR, gathered through row_index for grouped
-    // calls (those are kept in registers; plain calls recompute them).
-    int a_src[GROUPED ? A_LOADS : 1];
-    auto src_row = [&](int i) -> int {
-        const int c = tid + i * NT;
-        const int r = c / CPR;
-        if (c >= A_CHUNKS || r >= rows) return -1;
-        if constexpr (GROUPED) return a.row_index != nullptr ? a.row_index[row0 + r] : row0 + r;
-        return row0 + r;
-    };
-    if constexpr (GROUPED) {
-#pragma unroll
-        for (int i = 0; i < A_LOADS; ++i) a_src[i] = src_row(i);
-    }
-
-    u32x4_t ra[A_LOADS], rb[B_LOADS];
-    auto global_load = [&](int kt) {
-#pragma unroll
-        for (int i = 0; i < A_LOADS; ++i) {
-            const int c = tid + i * NT;
-            const int cc = c % CPR;
-            u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
-            const int src = GROUPED ? a_src[GROUPED ? i : 0] : src_row(i);
-            if (src >= 0) {
-                if constexpr (A8) {
-                    v = *reinterpret_cast<const u32x4_t*>(a.xq + (static_cast<int64_t>(src) * a.ktiles + kt) * kTileK +
-                                                          cc * 16);
-                } else {
-                    const int kk = kt * kTileK + cc * 8;
-                    if (kk < a.k) v = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<int64_t>(src) * a.k + kk);
-                }
-            }
-            ra[i] = v;
-        }
-#pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) {
-            const int c = tid + i * NT;
-            const int s = c / (TB / 16);
-            const int st = strip0 + s;
-            if (c < B_CHUNKS && st < a.strips)
-                rb[i] = *reinterpret_cast<const u32x4_t*>(wbase + (static_cast<int64_t>(st) * a.ktiles + kt) * TB +
-                                                          (c % (TB / 16)) * 16);
-            else
-                rb[i] = (F == PLM_INT4) ? u32x4_t{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u}
-                                        : u32x4_t{0u, 0u, 0u, 0u};
-        }
-    };
-    auto lds_store = [&]() {
-#pragma unroll
-        for (int i = 0; i < A_LOADS; ++i) {
-            const int c = tid + i * NT;
-            if (c < A_CHUNKS) *reinterpret_cast<u32x4_t*>(&lds[(c / CPR) * ALR + (c % CPR) * 16]) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) {
-            const int c = tid + i * NT;
-            if (c < B_CHUNKS) *reinterpret_cast<u32x4_t*>(&lds[A_BYTES + c * 16]) = rb[i];
-        }
-    };
-
-    auto scale_raw = [&](int j, int kt, int t) -> float {
-        const int g = UNIFORM ? kt * kTileK / a.group_size : (kt * kTileK + 32 * t + 8 * kq) / a.group_size;
-        const int st = min(strip0 + wn * NS + j, a.strips - 1);
-        const int64_t sidx = (static_cast<int64_t>(st) * a.groups + g) * a.scale_cols + (a.scale_cols == 1 ? 0 : col16);
-        return load_scale(sbase, sidx, a.scale_dtype);
-    };
-
+    uint32_t sc[NS][ST];
     if (kt_begin < kt_end) {
-        global_load(kt_begin);
-        lds_store();
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+#pragma unroll
+            for (int t = 0; t < ST; ++t) sc[j][t] = scale_bits(j, kt_begin, t);
+        issue(kt_begin, 0);
     }
-    __syncthreads();
 
     for (int kt = kt_begin; kt < kt_end; ++kt) {
-        if (kt + 1 < kt_end) global_load(kt + 1);
-
-        float sr[NS];
+        const int stage = (kt - kt_begin) & 1;
+        // This step's tiles have landed (they are the only loads in flight) and every
+        // wavefront is done with the other stage, which the next loads overwrite.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        uint32_t scn[NS][ST];
+        const bool more = kt + 1 < kt_end;
+        if (more) {
 #pragma unroll
-        for (int j = 0; j < NS; ++j) sr[j] = UNIFORM ? scale_raw(j, kt, 0) : 0.f;
+            for (int j = 0; j < NS; ++j)
+#pragma unroll
+                for (int t = 0; t < ST; ++t) scn[j][t] = scale_bits(j, kt + 1, t);
+            issue(kt + 1, stage ^ 1);
+        }
+
+        const uint8_t* sa = lds + stage * STAGE;
+        const uint8_t* sb = sa + A_STAGE;
         u32x4_t wv[NS][TB / 1024];
 #pragma unroll
         for (int j = 0; j < NS; ++j)
 #pragma unroll
             for (int h = 0; h < TB / 1024; ++h)
-                wv[j][h] = *reinterpret_cast<const u32x4_t*>(&lds[A_BYTES + (wn * NS + j) * TB + h * 1024 + lane * 16]);
+                wv[j][h] = *reinterpret_cast<const u32x4_t*>(sb + (wn * NS + j) * TB + h * 1024 + lane * 16);
 
         if constexpr (A8) {
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
-                const int row = wm * MT * 16 + i * 16 + col16;
-                const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(&lds[row * ALR + kq * 32]);
-                const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(&lds[row * ALR + kq * 32 + 16]);
+                const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
+                const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(ra + (((2 * kq) ^ (col16 & 7)) * 16));
+                const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(ra + (((2 * kq + 1) ^ (col16 & 7)) * 16));
                 const i32x8_t av = __builtin_bit_cast(i32x8_t, u32x8_cat(a0, a1));
 #pragma unroll
                 for (int j = 0; j < NS; ++j) {
                     const i32x8_t bv = __builtin_bit_cast(i32x8_t, u32x8_cat(wv[j][0], wv[j][TB / 1024 - 1]));
                     const f32x4_t part = mfma16x16x128_fp8(av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sr[j], part[r], acc[i][j][r]);
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(scale_from_bits<WIDE>(sc[j][0], bf16_scale), part[r], acc[i][j][r]);
                 }
             }
         } else {
@@ -222,12 +251,12 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
                 u32x4_t af[MT];
 #pragma unroll
                 for (int i = 0; i < MT; ++i) {
-                    const int row = wm * MT * 16 + i * 16 + col16;
-                    af[i] = *reinterpret_cast<const u32x4_t*>(&lds[row * ALR + (32 * t + 8 * kq) * 2]);
+                    const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
+                    af[i] = *reinterpret_cast<const u32x4_t*>(ra + (((4 * t + kq) ^ col16) * 16));
                 }
 #pragma unroll
                 for (int j = 0; j < NS; ++j) {
-                    const float raw = UNIFORM ? sr[j] : scale_raw(j, kt, t);
+                    const float raw = scale_from_bits<WIDE>(sc[j][UNIFORM ? 0 : t], bf16_scale);
                     u32x4_t b;
                     if constexpr (F == PLM_INT4) {
                         b = dq_int4<BF16>(wv[j][0][t], make_int4_scale<BF16>(raw));
@@ -240,10 +269,11 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
                 }
             }
         }
-        __syncthreads();
-        if (kt + 1 < kt_end) {
-            lds_store();
-            __syncthreads();
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < NS; ++j)
+#pragma unroll
+                for (int t = 0; t < ST; ++t) sc[j][t] = scn[j][t];
         }
     }
 
@@ -349,26 +379,32 @@ int64_t mfma_workspace_bytes(plm_format, int64_t m, int64_t n, int64_t k) {
 }
 
 namespace {
-template <plm_format F, bool BF16, bool UNIFORM, bool A8, bool GROUPED>
+template <plm_format F, bool BF16, bool UNIFORM, bool WIDE, bool A8, bool GROUPED>
 void launch_shape(const mfma_args& a, bool large, dim3 grid, hipStream_t s) {
     if (large)
-        mfma_kernel<F, BF16, UNIFORM, A8, GROUPED, kLarge.wm, kLarge.wn, kLarge.mt, kLarge.ns>
+        mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kLarge.wm, kLarge.wn, kLarge.mt, kLarge.ns>
             <<<grid, kLarge.wm * kLarge.wn * 64, 0, s>>>(a);
     else
-        mfma_kernel<F, BF16, UNIFORM, A8, GROUPED, kSmall.wm, kSmall.wn, kSmall.mt, kSmall.ns>
+        mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kSmall.wm, kSmall.wn, kSmall.mt, kSmall.ns>
             <<<grid, kSmall.wm * kSmall.wn * 64, 0, s>>>(a);
+}
+
+template <plm_format F, bool BF16, bool WIDE, bool GROUPED>
+void launch_mode_w(const mfma_args& a, bool large, bool uniform, bool a8, dim3 grid, hipStream_t s) {
+    if constexpr (F == PLM_FP8 && !GROUPED) {
+        if (a8) {
+            launch_shape<F, BF16, true, WIDE, true, GROUPED>(a, large, grid, s);
+            return;
+        }
+    }
+    if (uniform) launch_shape<F, BF16, true, WIDE, false, GROUPED>(a, large, grid, s);
+    else launch_shape<F, BF16, false, WIDE, false, GROUPED>(a, large, grid, s);
 }
 
 template <plm_format F, bool BF16, bool GROUPED>
 void launch_mode(const mfma_args& a, bool large, bool uniform, bool a8, dim3 grid, hipStream_t s) {
-    if constexpr (F == PLM_FP8 && !GROUPED) {
-        if (a8) {
-            launch_shape<F, BF16, true, true, GROUPED>(a, large, grid, s);
-            return;
-        }
-    }
-    if (uniform) launch_shape<F, BF16, true, false, GROUPED>(a, large, grid, s);
-    else launch_shape<F, BF16, false, false, GROUPED>(a, large, grid, s);
+    if (a.scale_dtype == PLM_FP32) launch_mode_w<F, BF16, true, GROUPED>(a, large, uniform, a8, grid, s);
+    else launch_mode_w<F, BF16, false, GROUPED>(a, large, uniform, a8, grid, s);
 }
 
 template <bool GROUPED>
@@ -405,6 +441,7 @@ void fill_common(mfma_args& a, const void* x, const void* w, const void* scale, 
 int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                 plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y,
                 void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq, const float* x_scale) {
+    PLM_CHECK_ARG(k <= (int64_t{1} << 21), op, "K above 2^21 is not supported");
     const mfma_config c = choose_mfma(m, n, k);
     mfma_args a{};
     fill_common(a, x, w, scale, scale_dtype, m, n, k, block_n, group_size, y);
@@ -433,11 +470,11 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
 // rows are in the grouped (sorted) order and `row_index` optionally gathers them from x.
 // shape indexes kGroupedShapes (int4 experts only).
 namespace {
-template <bool BF16, bool UNIFORM>
+template <bool BF16, bool UNIFORM, bool WIDE>
 void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
 #define PLM_GROUPED_CASE(i)                                                                                   \
     case i:                                                                                                   \
-        mfma_kernel<PLM_INT4, BF16, UNIFORM, false, true, kGroupedShapes[i].wm, kGroupedShapes[i].wn,         \
+        mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kGroupedShapes[i].wm, kGroupedShapes[i].wn,         \
                     kGroupedShapes[i].mt, kGroupedShapes[i].ns>                                               \
             <<<grid, kGroupedShapes[i].wm * kGroupedShapes[i].wn * 64, 0, s>>>(a);                            \
         break;
@@ -446,7 +483,7 @@ void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t 
         PLM_GROUPED_CASE(1)
         PLM_GROUPED_CASE(2)
         default:
-            mfma_kernel<PLM_INT4, BF16, UNIFORM, false, true, kLarge.wm, kLarge.wn, kLarge.mt, kLarge.ns>
+            mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kLarge.wm, kLarge.wn, kLarge.mt, kLarge.ns>
                 <<<grid, kLarge.wm * kLarge.wn * 64, 0, s>>>(a);
     }
 #undef PLM_GROUPED_CASE
@@ -469,7 +506,8 @@ int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const
                    void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* row_index, int shape,
                    hipStream_t s) {
     PLM_CHECK_ARG(f == PLM_INT4, op, "grouped GEMMs take int4 experts");
-    PLM_CHECK_ARG(rows < (int64_t{1} << 31) / 2 && n * k < (int64_t{1} << 40), op, "problem too large");
+    PLM_CHECK_ARG(k <= (int64_t{1} << 21) && rows * k * 2 < kOOB && n * k < (int64_t{1} << 40), op,
+                  "problem too large");
     mfma_args a{};
     fill_common(a, x, w, scale, scale_dtype, rows, n, k, block_n, group_size, y);
     const struct shape sh = kGroupedShapes[std::min(std::max(shape, 0), 3)];
@@ -483,8 +521,18 @@ int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const
     a.s_expert_bytes = static_cast<int64_t>(a.strips) * a.groups * a.scale_cols * dtype_size(scale_dtype);
     dim3 grid(static_cast<unsigned>(max_tiles * a.n_blocks), 1);
     const bool uniform = group_size % kTileK == 0;
-    if (bf16) uniform ? launch_grouped_shape<true, true>(a, shape, grid, s) : launch_grouped_shape<true, false>(a, shape, grid, s);
-    else uniform ? launch_grouped_shape<false, true>(a, shape, grid, s) : launch_grouped_shape<false, false>(a, shape, grid, s);
+    const bool wide = scale_dtype == PLM_FP32;
+    const int mode = (bf16 ? 4 : 0) + (uniform ? 2 : 0) + (wide ? 1 : 0);
+    switch (mode) {
+        case 0: launch_grouped_shape<false, false, false>(a, shape, grid, s); break;
+        case 1: launch_grouped_shape<false, false, true>(a, shape, grid, s); break;
+        case 2: launch_grouped_shape<false, true, false>(a, shape, grid, s); break;
+        case 3: launch_grouped_shape<false, true, true>(a, shape, grid, s); break;
+        case 4: launch_grouped_shape<true, false, false>(a, shape, grid, s); break;
+        case 5: launch_grouped_shape<true, false, true>(a, shape, grid, s); break;
+        case 6: launch_grouped_shape<true, true, false>(a, shape, grid, s); break;
+        default: launch_grouped_shape<true, true, true>(a, shape, grid, s); break;
+    }
     PLM_HIP_LAUNCH_CHECK(op);
     return PLM_OK;
 }

@@ -241,6 +241,13 @@ __device__ __forceinline__ uint32_t buffer_load_u32(__amdgpu_buffer_rsrc_t r, in
     return __builtin_amdgcn_raw_buffer_load_b32(r, voffset, soffset, 0);
 }
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// 16 bytes per lane from a buffer straight into LDS (no VGPR staging): lane L writes
+// lds + 16 * L, so `lds` (wave-uniform) is the base of the wavefront's 1 KiB. Counts in vmcnt;
+// out-of-range lanes write zeros.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voffset, int soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0,
+                                             0);
+}
 
 // Scale bits as loaded (16-bit fp16/bf16 zero-extended, or fp32) -> fp32.
 template <bool WIDE> __device__ __forceinline__ float scale_from_bits(uint32_t bits, bool bf16_storage) {

@@ -230,9 +230,12 @@ def _check_full(y, x, wd):
     rel = (torch.linalg.vector_norm(y.float() - ref) / torch.linalg.vector_norm(ref)).item()
     assert rel <= 5e-3, rel
     # Row checksums: sum_n y[m, n] against x[m] . sum_n W[n, :] (fp64), a property that does
-    # not depend on how the kernel tiles or splits K.
+    # not depend on how the kernel tiles or splits K. Each bf16 output carries at most half an
+    # ulp (2^-9 relative) of rounding, so a row sum may move by sum |y| * 2^-9; 2^-8 leaves room
+    # for the fp32 accumulation.
     cs = x.double() @ wd.double().sum(0)
-    assert torch.allclose(y.double().sum(1), cs, rtol=1e-2, atol=2e-2 * y.shape[1] ** 0.5)
+    bound = y.double().abs().sum(1) * 2.0**-8 + 1e-3
+    assert bool(((y.double().sum(1) - cs).abs() <= bound).all())
     return rel
 
 
