@@ -133,19 +133,28 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     // Chunk c of the A tile is rows c*RPC .. c*RPC+RPC-1; lane L of its load writes slot L % SLOTS
     // of row c*RPC + L / SLOTS, which holds the row's 16-byte column (slot ^ row % SLOTS): the XOR
     // swizzle puts the 16 rows of one MFMA fragment read in 16 different bank groups.
-    int a_off[A_PW], a_col[A_PW];
+    // Plain calls recompute the offsets per load (rows past `rows` fall outside the buffer);
+    // grouped calls keep the gathered ones in registers.
+    const int lrow = lane / SLOTS, lslot = lane % SLOTS;
+    int a_gather[GROUPED ? A_PW : 1];
+    if constexpr (GROUPED) {
 #pragma unroll
-    for (int i = 0; i < A_PW; ++i) {
-        const int r = (wave * A_PW + i) * RPC + lane / SLOTS;
-        const int c = (lane % SLOTS) ^ (r % SLOTS);
-        int src = -1;
-        if (r < rows) {
-            if constexpr (GROUPED) src = a.row_index != nullptr ? a.row_index[row0 + r] : row0 + r;
-            else src = r;
+        for (int i = 0; i < A_PW; ++i) {
+            const int r = (wave * A_PW + i) * RPC + lrow;
+            int src = -1;
+            if (r < rows) src = a.row_index != nullptr ? a.row_index[row0 + r] : row0 + r;
+            a_gather[i] = src < 0 ? kOOB : src * a_stride;
         }
-        a_off[i] = src < 0 ? kOOB : src * a_stride + c * 16;
-        a_col[i] = c * 8;  // bf16 elements into the K tile (tail check, bf16 only)
     }
+    auto a_offset = [&](int i, int kt) -> int {
+        const int r = (wave * A_PW + i) * RPC + lrow;
+        const int c = lslot ^ (r % SLOTS);
+        const int row_off = GROUPED ? a_gather[GROUPED ? i : 0] : r * a_stride;
+        if constexpr (!UNIFORM) {
+            if (kt * kTileK + c * 8 >= a.k) return kOOB;  // K tail (bf16 x only)
+        }
+        return row_off + c * 16;
+    };
     // Weights: this workgroup's strips are contiguous, ktiles * TB bytes each.
     const int strip_bytes = a.ktiles * TB;
     const __amdgpu_buffer_rsrc_t b_rsrc =
@@ -161,13 +170,8 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     auto issue = [&](int kt, int stage) {
         uint8_t* sa = lds + stage * STAGE;
 #pragma unroll
-        for (int i = 0; i < A_PW; ++i) {
-            int off = a_off[i];
-            if constexpr (!UNIFORM) {
-                if (kt * kTileK + a_col[i] >= a.k) off = kOOB;
-            }
-            buffer_load_lds16(a_rsrc, sa + (wave * A_PW + i) * 1024, off, kt * ARB);
-        }
+        for (int i = 0; i < A_PW; ++i)
+            buffer_load_lds16(a_rsrc, sa + (wave * A_PW + i) * 1024, a_offset(i, kt), kt * ARB);
 #pragma unroll
         for (int i = 0; i < B_PW; ++i)
             buffer_load_lds16(b_rsrc, sa + A_STAGE + (wave * B_PW + i) * 1024, b_off[i], kt * TB);
@@ -248,24 +252,25 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         } else {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                u32x4_t af[MT];
-#pragma unroll
-                for (int i = 0; i < MT; ++i) {
-                    const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
-                    af[i] = *reinterpret_cast<const u32x4_t*>(ra + (((4 * t + kq) ^ col16) * 16));
-                }
+                // Dequantize this 32-wide K slice of every strip once, then stream the x
+                // fragments past it: each weight fragment feeds MT MFMAs.
+                u32x4_t b[NS];
 #pragma unroll
                 for (int j = 0; j < NS; ++j) {
                     const float raw = scale_from_bits<WIDE>(sc[j][UNIFORM ? 0 : t], bf16_scale);
-                    u32x4_t b;
                     if constexpr (F == PLM_INT4) {
-                        b = dq_int4<BF16>(wv[j][0][t], make_int4_scale<BF16>(raw));
+                        b[j] = dq_int4<BF16>(wv[j][0][t], make_int4_scale<BF16>(raw));
                     } else {
-                        b = dq_fp8<BF16>(wv[j][t >> 1][(t & 1) * 2], wv[j][t >> 1][(t & 1) * 2 + 1],
-                                         round_to<BF16>(raw));
+                        b[j] = dq_fp8<BF16>(wv[j][t >> 1][(t & 1) * 2], wv[j][t >> 1][(t & 1) * 2 + 1],
+                                            round_to<BF16>(raw));
                     }
+                }
 #pragma unroll
-                    for (int i = 0; i < MT; ++i) acc[i][j] = mfma16x16x32<BF16>(af[i], b, acc[i][j]);
+                for (int i = 0; i < MT; ++i) {
+                    const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
+                    const u32x4_t af = *reinterpret_cast<const u32x4_t*>(ra + (((4 * t + kq) ^ col16) * 16));
+#pragma unroll
+                    for (int j = 0; j < NS; ++j) acc[i][j] = mfma16x16x32<BF16>(af, b[j], acc[i][j]);
                 }
             }
         }
@@ -289,24 +294,36 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
             }
     }
 
-    // Epilogue: lane holds column col16 of strip (strip0 + wn*NS + j), rows 4*kq + r of m tile i.
-    const int64_t mn = static_cast<int64_t>(a.m) * a.n;
-    if (a.splits == 1) {
+    // Split K: every workgroup stores its accumulators in lane order (16 bytes per lane per
+    // MFMA tile, so each store instruction is one contiguous 1 KiB) into its own slot of the
+    // work tile's partial area; the last workgroup to arrive reloads all slots and sums them
+    // in split order, so the result does not depend on arrival order.
+    if (a.splits > 1) {
+        constexpr int TILE_BYTES = MT * NS * NT * 16;
+        const __amdgpu_buffer_rsrc_t p_rsrc = make_rsrc(
+            reinterpret_cast<uint8_t*>(a.partial) + static_cast<int64_t>(blockIdx.x) * a.splits * TILE_BYTES,
+            static_cast<uint32_t>(a.splits * TILE_BYTES));
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
-            for (int j = 0; j < NS; ++j) {
-                const int col = (strip0 + wn * NS + j) * kTileN + col16;
+            for (int j = 0; j < NS; ++j)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[i][j]), p_rsrc,
+                                                       ((i * NS + j) * NT + tid) * 16, split * TILE_BYTES, kCoherent);
+        if (!arrive_last(&a.counters[blockIdx.x], static_cast<uint32_t>(a.splits), &last_flag)) return;
+        for (int sp = 0; sp < a.splits; ++sp) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int lr = wm * MT * 16 + i * 16 + 4 * kq + r;
-                    if (lr < rows && col < a.n)
-                        a.y[static_cast<int64_t>(row0 + lr) * a.n + col] =
-                            static_cast<uint16_t>(to_bits16<BF16>(acc[i][j][r]));
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NS; ++j) {
+                    const f32x4_t v = __builtin_bit_cast(
+                        f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(p_rsrc, ((i * NS + j) * NT + tid) * 16,
+                                                                       sp * TILE_BYTES, kCoherent));
+                    acc[i][j] = sp == 0 ? v : acc[i][j] + v;
                 }
-            }
-        return;
+        }
     }
+
+    // Epilogue: lane holds column col16 of strip (strip0 + wn*NS + j), rows 4*kq + r of m tile i.
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -316,21 +333,10 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
             for (int r = 0; r < 4; ++r) {
                 const int lr = wm * MT * 16 + i * 16 + 4 * kq + r;
                 if (lr < rows && col < a.n)
-                    store_partial(&a.partial[split * mn + static_cast<int64_t>(row0 + lr) * a.n + col], acc[i][j][r]);
+                    a.y[static_cast<int64_t>(row0 + lr) * a.n + col] =
+                        static_cast<uint16_t>(to_bits16<BF16>(acc[i][j][r]));
             }
         }
-    if (!arrive_last(&a.counters[blockIdx.x], static_cast<uint32_t>(a.splits), &last_flag)) return;
-    // Sum this tile's partials in split order; threads sweep the tile row-major.
-    for (int e = tid; e < BM * BS * kTileN; e += NT) {
-        const int lr = e / (BS * kTileN);
-        const int col = strip0 * kTileN + e % (BS * kTileN);
-        if (lr < rows && col < a.n) {
-            const int64_t off = static_cast<int64_t>(row0 + lr) * a.n + col;
-            float s = 0.f;
-            for (int sp = 0; sp < a.splits; ++sp) s += load_partial(&a.partial[sp * mn + off]);
-            a.y[off] = static_cast<uint16_t>(to_bits16<BF16>(s));
-        }
-    }
 }
 
 // Tile shapes: {WM, WN, MT, NS}.
@@ -339,29 +345,33 @@ struct shape {
     constexpr int bm() const { return wm * mt * 16; }
     constexpr int bs() const { return wn * ns; }
 };
-constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts (one per SIMD, 512 registers)
+constexpr shape kHuge{2, 4, 8, 4};   // 256 x 256, 8 wavefronts (int4 only: two stages fill the 160 KiB LDS)
+constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts
 constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
 // Grouped calls also use short row blocks for experts with few rows.
 constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
 constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
 constexpr shape kGroupedShapes[4] = {kRows16, kRows64, kSmall, kLarge};
+constexpr shape shape_of(int id) { return id == 2 ? kHuge : id == 1 ? kLarge : kSmall; }
 
 }  // namespace
 
 struct mfma_config {
-    bool large;
+    int shape;  // 0 small, 1 large, 2 huge
     int m_blocks, n_blocks;
     int splits, tiles_per_split;
 };
 
-mfma_config choose_mfma(int64_t m, int64_t n, int64_t k) {
+mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
     mfma_config c{};
     const int64_t cus = cu_count();
     const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
     const int64_t large_tiles = ceil_div(m, kLarge.bm()) * ceil_div(strips, kLarge.bs());
-    c.large = large_tiles >= cus;
-    if (const char* env = getenv("PLM_MFMA")) c.large = env[0] == 'L';  // tuning sweeps
-    const shape sh = c.large ? kLarge : kSmall;
+    const int64_t huge_tiles = ceil_div(m, kHuge.bm()) * ceil_div(strips, kHuge.bs());
+    c.shape = (f == PLM_INT4 && huge_tiles >= cus) ? 2 : large_tiles >= cus ? 1 : 0;
+    if (const char* env = getenv("PLM_MFMA")) c.shape = env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : 0;  // tuning sweeps
+    if (c.shape == 2 && f != PLM_INT4) c.shape = 1;
+    const shape sh = shape_of(c.shape);
     c.m_blocks = static_cast<int>(ceil_div(m, sh.bm()));
     c.n_blocks = static_cast<int>(ceil_div(strips, sh.bs()));
     const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
@@ -372,16 +382,25 @@ mfma_config choose_mfma(int64_t m, int64_t n, int64_t k) {
     return c;
 }
 
-int64_t mfma_workspace_bytes(plm_format, int64_t m, int64_t n, int64_t k) {
-    const mfma_config c = choose_mfma(m, n, k);
+int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k) {
+    const mfma_config c = choose_mfma(f, m, n, k);
     if (c.splits <= 1) return 0;
-    return kCounterBytes + static_cast<int64_t>(c.splits) * m * n * 4;
+    const shape sh = shape_of(c.shape);
+    const int64_t tile_bytes = static_cast<int64_t>(sh.bm()) * sh.bs() * kTileN * 4;
+    return kCounterBytes + static_cast<int64_t>(c.m_blocks) * c.n_blocks * c.splits * tile_bytes;
 }
 
 namespace {
 template <plm_format F, bool BF16, bool UNIFORM, bool WIDE, bool A8, bool GROUPED>
-void launch_shape(const mfma_args& a, bool large, dim3 grid, hipStream_t s) {
-    if (large)
+void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
+    if constexpr (F == PLM_INT4 && !A8 && !GROUPED) {
+        if (shape == 2) {
+            mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kHuge.wm, kHuge.wn, kHuge.mt, kHuge.ns>
+                <<<grid, kHuge.wm * kHuge.wn * 64, 0, s>>>(a);
+            return;
+        }
+    }
+    if (shape >= 1)
         mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kLarge.wm, kLarge.wn, kLarge.mt, kLarge.ns>
             <<<grid, kLarge.wm * kLarge.wn * 64, 0, s>>>(a);
     else
@@ -390,7 +409,7 @@ void launch_shape(const mfma_args& a, bool large, dim3 grid, hipStream_t s) {
 }
 
 template <plm_format F, bool BF16, bool WIDE, bool GROUPED>
-void launch_mode_w(const mfma_args& a, bool large, bool uniform, bool a8, dim3 grid, hipStream_t s) {
+void launch_mode_w(const mfma_args& a, int large, bool uniform, bool a8, dim3 grid, hipStream_t s) {
     if constexpr (F == PLM_FP8 && !GROUPED) {
         if (a8) {
             launch_shape<F, BF16, true, WIDE, true, GROUPED>(a, large, grid, s);
@@ -402,13 +421,13 @@ void launch_mode_w(const mfma_args& a, bool large, bool uniform, bool a8, dim3 g
 }
 
 template <plm_format F, bool BF16, bool GROUPED>
-void launch_mode(const mfma_args& a, bool large, bool uniform, bool a8, dim3 grid, hipStream_t s) {
+void launch_mode(const mfma_args& a, int large, bool uniform, bool a8, dim3 grid, hipStream_t s) {
     if (a.scale_dtype == PLM_FP32) launch_mode_w<F, BF16, true, GROUPED>(a, large, uniform, a8, grid, s);
     else launch_mode_w<F, BF16, false, GROUPED>(a, large, uniform, a8, grid, s);
 }
 
 template <bool GROUPED>
-void launch_all(plm_format f, bool bf16, const mfma_args& a, bool large, bool uniform, bool a8, dim3 grid,
+void launch_all(plm_format f, bool bf16, const mfma_args& a, int large, bool uniform, bool a8, dim3 grid,
                 hipStream_t s) {
     if (f == PLM_INT4) {
         if (bf16) launch_mode<PLM_INT4, true, GROUPED>(a, large, uniform, a8, grid, s);
@@ -442,7 +461,7 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
                 plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y,
                 void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq, const float* x_scale) {
     PLM_CHECK_ARG(k <= (int64_t{1} << 21), op, "K above 2^21 is not supported");
-    const mfma_config c = choose_mfma(m, n, k);
+    const mfma_config c = choose_mfma(f, m, n, k);
     mfma_args a{};
     fill_common(a, x, w, scale, scale_dtype, m, n, k, block_n, group_size, y);
     a.splits = c.splits;
@@ -461,7 +480,7 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
         a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     }
     dim3 grid(c.m_blocks * c.n_blocks, c.splits);
-    launch_all<false>(f, bf16, a, c.large, group_size % kTileK == 0, xq != nullptr, grid, s);
+    launch_all<false>(f, bf16, a, c.shape, group_size % kTileK == 0, xq != nullptr, grid, s);
     PLM_HIP_LAUNCH_CHECK(op);
     return PLM_OK;
 }

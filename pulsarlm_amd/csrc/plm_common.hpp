@@ -97,14 +97,12 @@ __device__ __forceinline__ f32x4_t mfma16x16x128_fp8(i32x8_t a, i32x8_t b, f32x4
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
+// Round to nearest even with gfx950's v_cvt_pk_bf16_f32 (a NaN stays a quiet NaN).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    // Round to nearest even; NaN stays NaN (quiet bit forced).
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-    return ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) & 0xffffu;
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f)));
 }
 
-__device__ __forceinline__ float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+__device__ __forceinline__ float round_bf16(float f) { return static_cast<float>(static_cast<__bf16>(f)); }
 
 __device__ __forceinline__ float round_f16(float f) { return static_cast<float>(static_cast<_Float16>(f)); }
 
@@ -271,6 +269,9 @@ template <bool WIDE> __device__ __forceinline__ uint32_t load_scale_bits(const v
 // cache) is needed: a workgroup waits for its own stores to complete, then one
 // lane counts the arrival.
 // ---------------------------------------------------------------------------
+// Cache policy of buffer loads/stores that must be coherent across XCDs (sc1): the same
+// policy agent-scope atomics get.
+constexpr int kCoherent = 16;
 __device__ __forceinline__ void store_partial(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
