@@ -352,34 +352,54 @@ constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
 constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
 constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
 constexpr shape kGroupedShapes[4] = {kRows16, kRows64, kSmall, kLarge};
-constexpr shape shape_of(int id) { return id == 2 ? kHuge : id == 1 ? kLarge : kSmall; }
+constexpr shape shape_of(int id) { return id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall; }
+// Relative MFMA throughput per unit of tile area, measured on MI355X at the Qwen3-8B shapes.
+constexpr double kShapeRate[4] = {0.75, 0.7, 1.0, 0.65};
 
 }  // namespace
 
 struct mfma_config {
-    int shape;  // 0 small, 1 large, 2 huge
+    int shape;  // 0 small, 1 large, 2 huge, 3 rows64
     int m_blocks, n_blocks;
     int splits, tiles_per_split;
 };
 
+// Tile shape and split count: the candidate with the least estimated time, counting whole
+// rounds of workgroups over the CUs and a fixed cost of about three K tiles per workgroup
+// (pipeline fill, epilogue, split-K reduction).
 mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
-    mfma_config c{};
     const int64_t cus = cu_count();
     const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
-    const int64_t large_tiles = ceil_div(m, kLarge.bm()) * ceil_div(strips, kLarge.bs());
-    const int64_t huge_tiles = ceil_div(m, kHuge.bm()) * ceil_div(strips, kHuge.bs());
-    c.shape = (f == PLM_INT4 && huge_tiles >= cus) ? 2 : large_tiles >= cus ? 1 : 0;
-    if (const char* env = getenv("PLM_MFMA")) c.shape = env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : 0;  // tuning sweeps
-    if (c.shape == 2 && f != PLM_INT4) c.shape = 1;
-    const shape sh = shape_of(c.shape);
-    c.m_blocks = static_cast<int>(ceil_div(m, sh.bm()));
-    c.n_blocks = static_cast<int>(ceil_div(strips, sh.bs()));
-    const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
-    int64_t splits = 1;
-    if (tiles < cus && tiles <= kMaxCounters) splits = std::min<int64_t>(ceil_div(cus, tiles), ktiles);
-    c.tiles_per_split = static_cast<int>(ceil_div(ktiles, splits));
-    c.splits = static_cast<int>(ceil_div(ktiles, c.tiles_per_split));
-    return c;
+    auto config = [&](int id) {
+        const shape sh = shape_of(id);
+        mfma_config c{};
+        c.shape = id;
+        c.m_blocks = static_cast<int>(ceil_div(m, sh.bm()));
+        c.n_blocks = static_cast<int>(ceil_div(strips, sh.bs()));
+        const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
+        int64_t splits = 1;
+        if (tiles < cus && tiles <= kMaxCounters)
+            splits = std::max<int64_t>(1, std::min<int64_t>(ceil_div(cus, tiles), ktiles / 4));
+        c.tiles_per_split = static_cast<int>(ceil_div(ktiles, splits));
+        c.splits = static_cast<int>(ceil_div(ktiles, c.tiles_per_split));
+        return c;
+    };
+    auto cost = [&](const mfma_config& c) {
+        const shape sh = shape_of(c.shape);
+        const int64_t rounds = ceil_div(static_cast<int64_t>(c.m_blocks) * c.n_blocks * c.splits, cus);
+        return static_cast<double>(rounds) * (c.tiles_per_split + 3) * sh.bm() * sh.bs() / kShapeRate[c.shape];
+    };
+    if (const char* env = getenv("PLM_MFMA")) {  // tuning sweeps: S, L, H or R
+        const int id = env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : 0;
+        return config(id == 2 && f != PLM_INT4 ? 1 : id);
+    }
+    mfma_config best = config(0);
+    for (int id = 1; id < 4; ++id) {
+        if (id == 2 && f != PLM_INT4) continue;
+        const mfma_config c = config(id);
+        if (cost(c) < cost(best)) best = c;
+    }
+    return best;
 }
 
 int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k) {
@@ -400,7 +420,10 @@ void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
             return;
         }
     }
-    if (shape >= 1)
+    if (shape == 3)
+        mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kRows64.wm, kRows64.wn, kRows64.mt, kRows64.ns>
+            <<<grid, kRows64.wm * kRows64.wn * 64, 0, s>>>(a);
+    else if (shape >= 1)
         mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kLarge.wm, kLarge.wn, kLarge.mt, kLarge.ns>
             <<<grid, kLarge.wm * kLarge.wn * 64, 0, s>>>(a);
     else
