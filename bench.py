@@ -166,13 +166,15 @@ def section_decode(b: Bench, steps, warmup, detail_shapes=True):
     ys = {(m, n): torch.empty(m, n, device=b.dev, dtype=torch.bfloat16) for m in DECODE_M for (_, _, n) in SHAPES}
 
     def launches_for(names, ms, copies):
+        # Every launch reads a weight copy that no launch of the last ~500 MB touched, so
+        # neither L2 nor the MALL serves weights (no layer is re-read for the next M).
         out = []
         for c in range(copies):
-            for name, k, n in SHAPES:
-                if name not in names:
-                    continue
-                w, s = layers[name][c % len(layers[name])]
-                for m in ms:
+            for mi, m in enumerate(ms):
+                for name, k, n in SHAPES:
+                    if name not in names:
+                        continue
+                    w, s = layers[name][(c * len(ms) + mi) % len(layers[name])]
                     out.append(b.gemm_launch(L.PLM_INT4, xs[(m, k)], w, s, L.PLM_FP16, m, n, k, 1, ys[(m, n)]))
         return out
 

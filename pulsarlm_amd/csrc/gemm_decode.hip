@@ -39,6 +39,8 @@ struct decode_args {
     // W8A8 only: e4m3 x in the lane-permuted layout [M][ktiles][128] and per-row scales.
     const uint8_t* xq;
     const float* x_scale;
+    // x staged in LDS (M <= 4): bytes per row and per wavefront of the staging area.
+    int xs_row, xs_wave;
 };
 
 // One wavefront's batch of TPW K tiles for SP strips: weights, raw scale bits and x.
@@ -61,7 +63,7 @@ template <plm_format F, int SP, int TPW, bool A8> struct decode_batch {
 // K tile is one v_mfma_scale_f32_16x16x128_f8f6f4 per strip on the raw weight bytes,
 // the tile's partial is multiplied by its fp32 block scale, and the row scale is
 // applied before the reduction.
-template <plm_format F, bool BF16, int SP, int TPW, int NW, bool UNIFORM, bool WIDE, bool A8 = false>
+template <plm_format F, bool BF16, int SP, int TPW, int NW, bool UNIFORM, bool WIDE, bool A8 = false, bool XS = false>
 __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
     constexpr int TB = fmt_traits<F>::tile_bytes;
     constexpr int ES = WIDE ? 4 : 2;  // scale element bytes
@@ -117,7 +119,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
             if constexpr (A8) {
                 b.x[tt][0] = buffer_load16(xr, x_lane, x_off);
                 b.x[tt][1] = buffer_load16(xr, x_lane + 16, x_off);
-            } else {
+            } else if constexpr (!XS) {
 #pragma unroll
                 for (int t = 0; t < 4; ++t) b.x[tt][t] = buffer_load16(xr, x_lane + 64 * t, x_off);
             }
@@ -127,6 +129,22 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
     f32x4_t acc[SP];
 #pragma unroll
     for (int j = 0; j < SP; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // XS: the wavefront copies its K range of x (rows < M, xs_row bytes each) into its own
+    // LDS area with buffer loads to LDS, 1 KiB per instruction, instead of issuing four
+    // mostly-empty 16-byte loads per K tile; the MFMA fragments are then read from LDS.
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs_lds[];
+    uint8_t* xs_wave = xs_lds + wave * a.xs_wave;
+    if constexpr (XS) {
+        const int total = a.m * a.xs_row;
+        for (int c = 0; c * 1024 < total; ++c) {  // wave-uniform
+            const int o = c * 1024 + lane * 16;
+            const int row = o / a.xs_row, col = o - row * a.xs_row;
+            const int g = w_lo * kTileK * 2 + col;  // byte offset into the row
+            const int off = (row < a.m && g < a.k * 2) ? row * a.k * 2 + g : kOOB;
+            buffer_load_lds16(xr, xs_wave + c * 1024, off, 0);
+        }
+    }
 
     auto compute_batch = [&](const decode_batch<F, SP, TPW, A8>& b, int kt0) {
 #pragma unroll
@@ -146,8 +164,14 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
                 continue;
             }
             u32x4_t xs[4];
+            if constexpr (XS) {
+                const uint8_t* xr_lds = xs_wave + min(col16, a.m - 1) * a.xs_row + (kt - w_lo) * 256 + kq * 16;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) xs[t] = b.x[tt][t];
+                for (int t = 0; t < 4; ++t) xs[t] = *reinterpret_cast<const u32x4_t*>(xr_lds + 64 * t);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xs[t] = b.x[tt][t];
+            }
             if ((kt + 1) * kTileK > a.k) {  // wave-uniform: partial last tile, zero x past K
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
@@ -191,6 +215,13 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
     decode_batch<F, SP, TPW, A8> b;
     for (int kt = w_lo; kt < w_hi; kt += TPW) {
         load_batch(b, kt);
+        if constexpr (XS) {
+            // The staging copy was issued before this batch's loads (weights and, for
+            // uniform groups, scales): waiting until only those are outstanding means x has
+            // landed. Later batches find it long done.
+            constexpr int kBatchLoads = TPW * SP * (fmt_traits<F>::tile_bytes / 1024 + (UNIFORM ? 1 : 0));
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kBatchLoads) : "memory");
+        }
         compute_batch(b, kt);
     }
     if constexpr (A8) {  // row scales; rows past M are never stored
@@ -323,6 +354,17 @@ void launch_decode_t(const decode_args& a, int strip_groups, bool uniform, hipSt
             return;
         }
     }
+    if (a.xs_wave > 0) {  // x staged in LDS
+        const size_t lds = static_cast<size_t>(NW) * a.xs_wave;
+        if (uniform) {
+            if (wide) decode_kernel<F, BF16, SP, TPW, NW, true, true, false, true><<<grid, NW * 64, lds, s>>>(a);
+            else decode_kernel<F, BF16, SP, TPW, NW, true, false, false, true><<<grid, NW * 64, lds, s>>>(a);
+        } else {
+            if (wide) decode_kernel<F, BF16, SP, TPW, NW, false, true, false, true><<<grid, NW * 64, lds, s>>>(a);
+            else decode_kernel<F, BF16, SP, TPW, NW, false, false, false, true><<<grid, NW * 64, lds, s>>>(a);
+        }
+        return;
+    }
     if (uniform) {
         if (wide) decode_kernel<F, BF16, SP, TPW, NW, true, true><<<grid, NW * 64, 0, s>>>(a);
         else decode_kernel<F, BF16, SP, TPW, NW, true, false><<<grid, NW * 64, 0, s>>>(a);
@@ -354,6 +396,14 @@ void launch_decode_f(const decode_args& a, const decode_config& c, bool uniform,
 }
 }  // namespace
 
+// x rows are staged in LDS for M up to this (above it the 16-byte loads of x are mostly full).
+constexpr int64_t kStageMaxM = 4;
+constexpr int64_t kStageMaxBytes = 96 * 1024;  // staging area per workgroup
+bool no_x_staging() {
+    static const bool off = getenv("PLM_DECODE_NO_XS") != nullptr;  // A/B measurements
+    return off;
+}
+
 int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                   plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
                   void* y, void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq,
@@ -378,6 +428,11 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
     a.tiles_per_split = c.tiles_per_split;
     a.xq = xq;
     a.x_scale = x_scale;
+    if (m <= kStageMaxM && xq == nullptr && !no_x_staging()) {
+        a.xs_row = static_cast<int>(ceil_div(c.tiles_per_split, c.nw)) * kTileK * 2;
+        a.xs_wave = static_cast<int>(ceil_div(m * a.xs_row, 1024)) * 1024;
+        if (static_cast<int64_t>(c.nw) * a.xs_wave > kStageMaxBytes) a.xs_row = a.xs_wave = 0;  // long K: direct loads
+    }
     PLM_CHECK_ARG(c.splits > 0, op, "N = %lld is too large for the decode kernel", static_cast<long long>(n));
     // Buffer offsets stay below kOOB: x is at most 16 x K bf16, a weight strip K/128 tiles.
     PLM_CHECK_ARG(k <= (int64_t{1} << 24), op, "K must be at most 2^24");

@@ -78,9 +78,12 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     constexpr int A_STAGE = BM * ARB;
     constexpr int B_STAGE = BS * TB;
     constexpr int STAGE = A_STAGE + B_STAGE;
-    constexpr int A_PW = A_STAGE / 1024 / NW;  // 1 KiB chunks each wavefront loads per K step
-    constexpr int B_PW = B_STAGE / 1024 / NW;
-    static_assert(A_STAGE % (1024 * NW) == 0 && B_STAGE % (1024 * NW) == 0, "chunks split evenly over wavefronts");
+    constexpr int A_CHUNKS = A_STAGE / 1024, B_CHUNKS = B_STAGE / 1024;
+    constexpr int A_PW = (A_CHUNKS + NW - 1) / NW;  // 1 KiB chunks each wavefront loads per K step
+    constexpr int B_PW = (B_CHUNKS + NW - 1) / NW;
+    static_assert(A_STAGE % 1024 == 0 && B_STAGE % 1024 == 0, "stages are whole 1 KiB chunks");
+    static_assert((A_CHUNKS % NW == 0 || A_CHUNKS < NW) && (B_CHUNKS % NW == 0 || B_CHUNKS < NW),
+                  "chunks split evenly over the wavefronts that load them");
     constexpr int ST = UNIFORM ? 1 : 4;  // scale values per strip per K step
     constexpr int ES = WIDE ? 4 : 2;     // scale element bytes
 
@@ -171,10 +174,12 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         uint8_t* sa = lds + stage * STAGE;
 #pragma unroll
         for (int i = 0; i < A_PW; ++i)
-            buffer_load_lds16(a_rsrc, sa + (wave * A_PW + i) * 1024, a_offset(i, kt), kt * ARB);
+            if (A_CHUNKS >= NW || wave < A_CHUNKS)  // wave-uniform
+                buffer_load_lds16(a_rsrc, sa + (wave * A_PW + i) * 1024, a_offset(i, kt), kt * ARB);
 #pragma unroll
         for (int i = 0; i < B_PW; ++i)
-            buffer_load_lds16(b_rsrc, sa + A_STAGE + (wave * B_PW + i) * 1024, b_off[i], kt * TB);
+            if (B_CHUNKS >= NW || wave < B_CHUNKS)  // wave-uniform
+                buffer_load_lds16(b_rsrc, sa + A_STAGE + (wave * B_PW + i) * 1024, b_off[i], kt * TB);
     };
 
     // Scales of this workgroup's strips ([strip][group][scale_cols], ES bytes each), loaded as
@@ -352,14 +357,16 @@ constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
 constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
 constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
 constexpr shape kGroupedShapes[4] = {kRows16, kRows64, kSmall, kLarge};
-constexpr shape shape_of(int id) { return id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall; }
+constexpr shape shape_of(int id) {
+    return id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
+}
 // Relative MFMA throughput per unit of tile area, measured on MI355X at the Qwen3-8B shapes.
-constexpr double kShapeRate[4] = {0.75, 0.7, 1.0, 0.65};
+constexpr double kShapeRate[5] = {0.75, 0.7, 1.0, 0.65, 0.3};
 
 }  // namespace
 
 struct mfma_config {
-    int shape;  // 0 small, 1 large, 2 huge, 3 rows64
+    int shape;  // 0 small, 1 large, 2 huge, 3 rows64, 4 rows16
     int m_blocks, n_blocks;
     int splits, tiles_per_split;
 };
@@ -390,7 +397,7 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
         return static_cast<double>(rounds) * (c.tiles_per_split + 3) * sh.bm() * sh.bs() / kShapeRate[c.shape];
     };
     if (const char* env = getenv("PLM_MFMA")) {  // tuning sweeps: S, L, H or R
-        const int id = env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : 0;
+        const int id = env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : 0;
         return config(id == 2 && f != PLM_INT4 ? 1 : id);
     }
     mfma_config best = config(0);
@@ -420,7 +427,10 @@ void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
             return;
         }
     }
-    if (shape == 3)
+    if (shape == 4)
+        mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kRows16.wm, kRows16.wn, kRows16.mt, kRows16.ns>
+            <<<grid, kRows16.wm * kRows16.wn * 64, 0, s>>>(a);
+    else if (shape == 3)
         mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kRows64.wm, kRows64.wn, kRows64.mt, kRows64.ns>
             <<<grid, kRows64.wm * kRows64.wn * 64, 0, s>>>(a);
     else if (shape >= 1)
