@@ -306,10 +306,15 @@ decode_config choose_decode(plm_format f, int64_t m, int64_t n, int64_t k) {
     const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
     const int64_t cus = cu_count();
     // Measured on MI355X at the Qwen3-8B shapes (int4, g128): two strips per wavefront
-    // (halving the x traffic per weight byte) pays when there are many strips or M > 4;
-    // otherwise one strip and two K tiles per batch; 16 wavefronts split K.
+    // (halving the x traffic per weight byte) pays when there are many strips or M > 4,
+    // four when M > 4 and the strip groups still fill most of the GPU; otherwise one strip
+    // and two K tiles per batch; 16 wavefronts split K.
+    const int64_t groups4 = ceil_div(strips, 4);
+    const int64_t wgs4 = groups4 * std::min<int64_t>(ceil_div(cus, groups4), std::max<int64_t>(1, ktiles / 16));
     if (strips >= 4 * cus) {
         c.sp = 2, c.tpw = 1, c.nw = 16;
+    } else if (m > 4 && ktiles >= 32 && 4 * wgs4 >= 3 * cus) {
+        c.sp = 4, c.tpw = 1, c.nw = 16;
     } else if (m > 4) {
         c.sp = 2, c.tpw = 1, c.nw = 8;
     } else {
@@ -318,13 +323,14 @@ decode_config choose_decode(plm_format f, int64_t m, int64_t n, int64_t k) {
     if (ktiles < 2 * c.nw) c.nw = ktiles >= 16 ? 8 : 4;
     if (const char* env = getenv("PLM_DECODE")) {  // "sp,tpw,nw" for tuning sweeps
         int sp = 0, t = 0, nw = 0;
-        if (sscanf(env, "%d,%d,%d", &sp, &t, &nw) == 3 && (sp == 1 || sp == 2) && (t == 1 || t == 2) &&
+        if (sscanf(env, "%d,%d,%d", &sp, &t, &nw) == 3 && (sp == 1 || sp == 2 || sp == 4) && (t == 1 || t == 2) &&
             (nw == 4 || nw == 8 || nw == 16)) {
             c.sp = sp;
             c.tpw = t;
             c.nw = nw;
         }
     }
+    if (c.sp == 4 && (c.tpw != 1 || c.nw != 16)) c.sp = 2;  // four strips: one instantiation only
     (void)f;
     c.strip_groups = static_cast<int>(ceil_div(strips, c.sp));
     // Split K across workgroups only when the column blocks alone cannot fill the GPU.
@@ -392,7 +398,8 @@ void launch_decode_sp(const decode_args& a, const decode_config& c, bool uniform
 template <plm_format F, bool BF16>
 void launch_decode_f(const decode_args& a, const decode_config& c, bool uniform, hipStream_t s) {
     if (c.sp == 1) launch_decode_sp<F, BF16, 1>(a, c, uniform, s);
-    else launch_decode_sp<F, BF16, 2>(a, c, uniform, s);
+    else if (c.sp == 2) launch_decode_sp<F, BF16, 2>(a, c, uniform, s);
+    else launch_decode_t<F, BF16, 4, 1, 16>(a, c.strip_groups, uniform, s);
 }
 }  // namespace
 
