@@ -356,7 +356,7 @@ constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
 // Grouped calls also use short row blocks for experts with few rows.
 constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
 constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
-constexpr shape kGroupedShapes[4] = {kRows16, kRows64, kSmall, kLarge};
+constexpr shape kGroupedShapes[5] = {kRows16, kRows64, kSmall, kLarge, kHuge};
 constexpr shape shape_of(int id) {
     return id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
 }
@@ -520,7 +520,7 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
 
 // Grouped: `tiles` holds max_tiles (expert, first row, rows) records built on the device;
 // rows are in the grouped (sorted) order and `row_index` optionally gathers them from x.
-// shape indexes kGroupedShapes (int4 experts only).
+// shape indexes kGroupedShapes (int4 experts only); 4 (256 x 256) is for full blocks of rows.
 namespace {
 template <bool BF16, bool UNIFORM, bool WIDE>
 void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
@@ -534,15 +534,16 @@ void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t 
         PLM_GROUPED_CASE(0)
         PLM_GROUPED_CASE(1)
         PLM_GROUPED_CASE(2)
+        PLM_GROUPED_CASE(3)
         default:
-            mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kLarge.wm, kLarge.wn, kLarge.mt, kLarge.ns>
-                <<<grid, kLarge.wm * kLarge.wn * 64, 0, s>>>(a);
+            mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kHuge.wm, kHuge.wn, kHuge.mt, kHuge.ns>
+                <<<grid, kHuge.wm * kHuge.wn * 64, 0, s>>>(a);
     }
 #undef PLM_GROUPED_CASE
 }
 }  // namespace
 
-int grouped_block_rows(int shape) { return kGroupedShapes[std::min(std::max(shape, 0), 3)].bm(); }
+int grouped_block_rows(int shape) { return kGroupedShapes[std::min(std::max(shape, 0), 4)].bm(); }
 
 // Row block for a grouped call: about the average rows per expert.
 int grouped_shape_for(int64_t rows, int64_t n_experts) {
@@ -562,7 +563,7 @@ int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const
                   "problem too large");
     mfma_args a{};
     fill_common(a, x, w, scale, scale_dtype, rows, n, k, block_n, group_size, y);
-    const struct shape sh = kGroupedShapes[std::min(std::max(shape, 0), 3)];
+    const struct shape sh = kGroupedShapes[std::min(std::max(shape, 0), 4)];
     a.splits = 1;
     a.tiles_per_split = a.ktiles;
     a.m_blocks = 1;

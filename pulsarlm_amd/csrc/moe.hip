@@ -46,28 +46,61 @@ __global__ void __launch_bounds__(kChunk) moe_hist_kernel(const int32_t* __restr
     for (int e = threadIdx.x; e < n_experts; e += kChunk) counts[static_cast<int64_t>(blockIdx.x) * n_experts + e] = hist[e];
 }
 
-// One workgroup: per expert, exclusive scan over chunks (in place) and the total; then
-// an exclusive scan over experts for the start rows, and the inclusive-end offsets.
-__global__ void __launch_bounds__(1024) moe_scan_kernel(int32_t* __restrict__ counts, int n_chunks, int n_experts,
-                                                         int32_t* __restrict__ start, int32_t* __restrict__ offsets) {
-    extern __shared__ int32_t tot[];
-    for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
-        int32_t run = 0;
-        for (int c = 0; c < n_chunks; ++c) {
-            const int32_t v = counts[static_cast<int64_t>(c) * n_experts + e];
-            counts[static_cast<int64_t>(c) * n_experts + e] = run;
-            run += v;
+// Exclusive scan of v[0..n) into v (in place) by one workgroup of 1024 threads; returns the
+// total in every thread. `buf` holds 1024 ints of LDS.
+__device__ int32_t block_exclusive_scan(int32_t* v, int n, int32_t* buf) {
+    int32_t carry = 0;
+    for (int base = 0; base < n; base += 1024) {
+        const int i = base + threadIdx.x;
+        const int32_t x = i < n ? v[i] : 0;
+        buf[threadIdx.x] = x;
+        __syncthreads();
+        for (int d = 1; d < 1024; d <<= 1) {  // Hillis-Steele inclusive scan
+            const int32_t y = threadIdx.x >= static_cast<unsigned>(d) ? buf[threadIdx.x - d] : 0;
+            __syncthreads();
+            buf[threadIdx.x] += y;
+            __syncthreads();
         }
-        tot[e] = run;
+        if (i < n) v[i] = carry + buf[threadIdx.x] - x;
+        carry += buf[1023];
+        __syncthreads();
     }
+    return carry;
+}
+
+// Per expert (one workgroup each): exclusive scan of its chunk counts, in place, and the
+// expert's total.
+__global__ void __launch_bounds__(1024) moe_scan_chunks_kernel(int32_t* __restrict__ counts, int n_chunks,
+                                                                int n_experts, int32_t* __restrict__ totals) {
+    __shared__ int32_t buf[1024];
+    __shared__ int32_t col[4096];
+    const int e = blockIdx.x;
+    int32_t carry = 0;
+    for (int base = 0; base < n_chunks; base += 4096) {
+        const int len = min(4096, n_chunks - base);
+        for (int c = threadIdx.x; c < len; c += 1024) col[c] = counts[static_cast<int64_t>(base + c) * n_experts + e];
+        __syncthreads();
+        const int32_t tot = block_exclusive_scan(col, len, buf);
+        for (int c = threadIdx.x; c < len; c += 1024)
+            counts[static_cast<int64_t>(base + c) * n_experts + e] = carry + col[c];
+        carry += tot;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) totals[e] = carry;
+}
+
+// Start rows (exclusive scan over experts) and the inclusive-end offsets at::cumsum gives.
+__global__ void __launch_bounds__(1024) moe_scan_experts_kernel(const int32_t* __restrict__ totals, int n_experts,
+                                                                 int32_t* __restrict__ start,
+                                                                 int32_t* __restrict__ offsets) {
+    __shared__ int32_t buf[1024];
+    __shared__ int32_t v[4096];
+    for (int e = threadIdx.x; e < n_experts; e += 1024) v[e] = totals[e];
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int32_t run = 0;
-        for (int e = 0; e < n_experts; ++e) {
-            start[e] = run;
-            run += tot[e];
-            offsets[e] = run;
-        }
+    block_exclusive_scan(v, n_experts, buf);
+    for (int e = threadIdx.x; e < n_experts; e += 1024) {
+        start[e] = v[e];
+        offsets[e] = v[e] + totals[e];
     }
 }
 
@@ -97,18 +130,14 @@ __global__ void __launch_bounds__(kChunk) moe_scatter_kernel(const int32_t* __re
 // written at the expert's tile prefix; slots past the last tile get rows = 0.
 __global__ void __launch_bounds__(1024) moe_tiles_kernel(const int32_t* __restrict__ offsets, int n_experts, int bm,
                                                           int64_t max_tiles, int32_t* __restrict__ tiles) {
-    extern __shared__ int32_t first_tile[];
-    if (threadIdx.x == 0) {
-        int32_t run = 0, prev = 0;
-        for (int e = 0; e < n_experts; ++e) {
-            first_tile[e] = run;
-            const int32_t rows = offsets[e] - prev;
-            prev = offsets[e];
-            run += rows > 0 ? (rows + bm - 1) / bm : 0;
-        }
-        first_tile[n_experts] = run;
+    __shared__ int32_t buf[1024];
+    __shared__ int32_t first_tile[4096];
+    for (int e = threadIdx.x; e < n_experts; e += 1024) {
+        const int32_t rows = offsets[e] - (e == 0 ? 0 : offsets[e - 1]);
+        first_tile[e] = rows > 0 ? (rows + bm - 1) / bm : 0;
     }
     __syncthreads();
+    const int32_t n_tiles = block_exclusive_scan(first_tile, n_experts, buf);
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
         const int32_t lo = e == 0 ? 0 : offsets[e - 1], hi = offsets[e];
         int32_t t = first_tile[e];
@@ -118,45 +147,112 @@ __global__ void __launch_bounds__(1024) moe_tiles_kernel(const int32_t* __restri
             tiles[3 * t + 2] = min(bm, hi - r);
         }
     }
-    for (int64_t t = first_tile[n_experts] + threadIdx.x; t < max_tiles; t += blockDim.x) {
+    for (int64_t t = n_tiles + threadIdx.x; t < max_tiles; t += blockDim.x) {
         tiles[3 * t] = 0;
         tiles[3 * t + 1] = 0;
         tiles[3 * t + 2] = 0;
     }
 }
 
+// Two-level tile lists for skewed groups: expert e's rows in full blocks of 256 (a last
+// block of at least 192 rows counts as full) go to `big`, the remaining rows (< 192) to
+// `small` in blocks of 64. Slots past the last tile of either list get rows = 0.
+__device__ __forceinline__ void tiles2_split(int32_t c, int32_t& nbig, int32_t& rem) {
+    nbig = c / 256;
+    rem = c - nbig * 256;
+    if (rem >= 192) ++nbig, rem = 0;
+}
+
+__global__ void __launch_bounds__(1024) moe_tiles2_kernel(const int32_t* __restrict__ offsets, int n_experts,
+                                                           int64_t max_big, int64_t max_small,
+                                                           int32_t* __restrict__ big, int32_t* __restrict__ small) {
+    __shared__ int32_t buf[1024];
+    __shared__ int32_t first_big[4096];
+    __shared__ int32_t first_small[4096];
+    for (int e = threadIdx.x; e < n_experts; e += 1024) {
+        int32_t nbig, rem;
+        tiles2_split(offsets[e] - (e == 0 ? 0 : offsets[e - 1]), nbig, rem);
+        first_big[e] = nbig;
+        first_small[e] = (rem + 63) / 64;
+    }
+    __syncthreads();
+    const int32_t n_big = block_exclusive_scan(first_big, n_experts, buf);
+    const int32_t n_small = block_exclusive_scan(first_small, n_experts, buf);
+    for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
+        const int32_t lo = e == 0 ? 0 : offsets[e - 1], hi = offsets[e];
+        int32_t nbig, rem;
+        tiles2_split(hi - lo, nbig, rem);
+        int32_t r = lo, t = first_big[e];
+        for (int b = 0; b < nbig; ++b, ++t, r += 256) {
+            big[3 * t] = e;
+            big[3 * t + 1] = r;
+            big[3 * t + 2] = min(256, hi - r);
+        }
+        t = first_small[e];
+        for (; r < hi; r += 64, ++t) {
+            small[3 * t] = e;
+            small[3 * t + 1] = r;
+            small[3 * t + 2] = min(64, hi - r);
+        }
+    }
+    for (int64_t t = n_big + threadIdx.x; t < max_big; t += blockDim.x) big[3 * t + 2] = 0;
+    for (int64_t t = n_small + threadIdx.x; t < max_small; t += blockDim.x) small[3 * t + 2] = 0;
+}
+
 // act[r, i] = round(round(silu(g)) * u) with (g | u) = gu[r, :] (the reference's
-// at::silu(gate) * up in the activation dtype).
+// at::silu(gate) * up in the activation dtype). Eight values per thread (16-byte loads and
+// stores; inter % 8 == 0 is checked by the caller).
 template <bool BF16>
-__global__ void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t rows, int inter, uint16_t* __restrict__ act) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+__global__ void __launch_bounds__(256) silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t rows, int inter,
+                                                       uint16_t* __restrict__ act) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
     if (i >= rows * inter) return;
     const int64_t r = i / inter, c = i % inter;
-    const float g = from_bits16<BF16>(gu[r * 2 * inter + c]);
-    const float u = from_bits16<BF16>(gu[r * 2 * inter + inter + c]);
-    const float sg = round_to<BF16>(g / (1.f + __expf(-g)));
-    act[i] = static_cast<uint16_t>(to_bits16<BF16>(sg * u));
+    const u32x4_t g = *reinterpret_cast<const u32x4_t*>(gu + r * 2 * inter + c);
+    const u32x4_t u = *reinterpret_cast<const u32x4_t*>(gu + r * 2 * inter + inter + c);
+    u32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float v[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float gv = from_bits16<BF16>((g[q] >> (16 * h)) & 0xffffu);
+            const float uv = from_bits16<BF16>((u[q] >> (16 * h)) & 0xffffu);
+            v[h] = round_to<BF16>(gv / (1.f + __expf(-gv))) * uv;
+        }
+        o[q] = pack2<BF16>(v[0], v[1]);
+    }
+    *reinterpret_cast<u32x4_t*>(act + i) = o;
 }
 
 // out[t, h] = sum_j round(d[pos(t, j), h] * round(w[t, j])), summed in j order in fp32.
+// One workgroup per token (its positions and weights are wave-uniform); eight consecutive
+// h per thread (hidden % 8 == 0 is checked by the caller).
 template <bool BF16>
-__global__ void moe_combine_kernel(const uint16_t* __restrict__ d, const int32_t* __restrict__ position,
-                                   const float* __restrict__ weights, int64_t tokens, int top_k, int hidden,
-                                   uint16_t* __restrict__ out) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= tokens * hidden) return;
-    const int64_t t = i / hidden, h = i % hidden;
-    float acc = 0.f;
+__global__ void __launch_bounds__(256) moe_combine_kernel(const uint16_t* __restrict__ d,
+                                                          const int32_t* __restrict__ position,
+                                                          const float* __restrict__ weights, int top_k, int hidden,
+                                                          uint16_t* __restrict__ out) {
+    const int64_t t = blockIdx.x;
+    const int h = (blockIdx.y * blockDim.x + threadIdx.x) * 8;
+    if (h >= hidden) return;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < top_k; ++j) {
         const int32_t p = position[t * top_k + j];
         const float w = round_to<BF16>(weights[t * top_k + j]);
-        acc += round_to<BF16>(from_bits16<BF16>(d[static_cast<int64_t>(p) * hidden + h]) * w);
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(d + static_cast<int64_t>(p) * hidden + h);
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            acc[q] += round_to<BF16>(from_bits16<BF16>((v[q / 2] >> (16 * (q % 2))) & 0xffffu) * w);
     }
-    out[i] = static_cast<uint16_t>(to_bits16<BF16>(acc));
+    u32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = pack2<BF16>(acc[2 * q], acc[2 * q + 1]);
+    *reinterpret_cast<u32x4_t*>(out + t * hidden + h) = o;
 }
 
 struct moe_ws {
-    int64_t counts, start, sorted_token, sorted_weight, position, tiles, gu, act, d, total;
+    int64_t counts, totals, start, sorted_token, sorted_weight, position, tiles, gu, act, d, total;
 };
 
 int64_t align256(int64_t v) { return round_up(v, 256); }
@@ -172,6 +268,7 @@ moe_ws moe_layout(int64_t tokens, int64_t top_k, int64_t n_experts, int64_t hidd
         return at;
     };
     w.counts = take(chunks * n_experts * 4);
+    w.totals = take(n_experts * 4);
     w.start = take(n_experts * 4);
     w.sorted_token = take(rows * 4);
     w.sorted_weight = take(rows * 4);
@@ -184,10 +281,31 @@ moe_ws moe_layout(int64_t tokens, int64_t top_k, int64_t n_experts, int64_t hidd
     return w;
 }
 
-int64_t moe_max_tiles(int64_t rows, int64_t n_experts) {
-    const int bm = grouped_block_rows(grouped_shape_for(rows, n_experts));
-    return ceil_div(rows, bm) + n_experts;
+// How a grouped GEMM over `rows` sorted rows is tiled. With many rows per expert (skewed
+// routing at large batch), full 256-row blocks run on the 256 x 256 shape and the rest on
+// 64-row tiles (two launches); otherwise one shape sized to the average rows per expert.
+struct grouped_plan {
+    bool two;
+    int shape;
+    int64_t max_a, max_b;  // tile slots of the first and second list
+    int64_t slots() const { return max_a + max_b; }
+};
+
+grouped_plan plan_grouped(int64_t rows, int64_t n_experts) {
+    grouped_plan p{};
+    p.two = rows >= 128 * n_experts;
+    if (p.two) {
+        p.shape = 4;
+        p.max_a = rows / 192 + 1;
+        p.max_b = std::min<int64_t>(3 * n_experts, ceil_div(rows, 64));
+    } else {
+        p.shape = grouped_shape_for(rows, n_experts);
+        p.max_a = ceil_div(rows, grouped_block_rows(p.shape)) + n_experts;
+    }
+    return p;
 }
+
+int64_t moe_max_tiles(int64_t rows, int64_t n_experts) { return plan_grouped(rows, n_experts).slots(); }
 
 int launch_sort(const char* op, const int32_t* experts, const float* weights, int64_t rows, int64_t top_k,
                 int64_t n_experts, uint8_t* base, const moe_ws& l, int32_t* offsets, hipStream_t s) {
@@ -196,7 +314,10 @@ int launch_sort(const char* op, const int32_t* experts, const float* weights, in
     auto* start = reinterpret_cast<int32_t*>(base + l.start);
     const size_t hist_lds = static_cast<size_t>(n_experts) * 4;
     moe_hist_kernel<<<static_cast<unsigned>(chunks), kChunk, hist_lds, s>>>(experts, rows, int(n_experts), counts);
-    moe_scan_kernel<<<1, 1024, hist_lds, s>>>(counts, int(chunks), int(n_experts), start, offsets);
+    auto* totals = reinterpret_cast<int32_t*>(base + l.totals);
+    moe_scan_chunks_kernel<<<static_cast<unsigned>(n_experts), 1024, 0, s>>>(counts, int(chunks), int(n_experts),
+                                                                             totals);
+    moe_scan_experts_kernel<<<1, 1024, 0, s>>>(totals, int(n_experts), start, offsets);
     moe_scatter_kernel<<<static_cast<unsigned>(chunks), kChunk, 0, s>>>(
         experts, weights, rows, int(top_k), int(n_experts), counts, start,
         reinterpret_cast<int32_t*>(base + l.sorted_token), reinterpret_cast<float*>(base + l.sorted_weight),
@@ -205,12 +326,25 @@ int launch_sort(const char* op, const int32_t* experts, const float* weights, in
     return PLM_OK;
 }
 
-int launch_tiles(const char* op, const int32_t* offsets, int64_t n_experts, int bm, int64_t max_tiles, int32_t* tiles,
+int launch_tiles(const char* op, const int32_t* offsets, int64_t n_experts, const grouped_plan& p, int32_t* tiles,
                  hipStream_t s) {
-    moe_tiles_kernel<<<1, 1024, static_cast<size_t>(n_experts + 1) * 4, s>>>(offsets, int(n_experts), bm, max_tiles,
-                                                                              tiles);
+    if (p.two)
+        moe_tiles2_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), p.max_a, p.max_b, tiles, tiles + 3 * p.max_a);
+    else
+        moe_tiles_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), grouped_block_rows(p.shape), p.max_a, tiles);
     PLM_HIP_LAUNCH_CHECK(op);
     return PLM_OK;
+}
+
+int launch_plan(const char* op, const grouped_plan& p, const void* x, bool bf16, const void* w, const void* scale,
+                plm_dtype scale_dtype, int64_t rows, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                void* y, const int32_t* tiles, const int32_t* row_index, hipStream_t s) {
+    if (int rc = launch_grouped(op, PLM_INT4, x, bf16, w, scale, scale_dtype, rows, n, k, block_n, group_size, y,
+                                tiles, p.max_a, row_index, p.shape, s))
+        return rc;
+    if (!p.two) return PLM_OK;
+    return launch_grouped(op, PLM_INT4, x, bf16, w, scale, scale_dtype, rows, n, k, block_n, group_size, y,
+                          tiles + 3 * p.max_a, p.max_b, row_index, 1, s);
 }
 
 }  // namespace
@@ -237,24 +371,23 @@ int plm_grouped_gemm(plm_format format, const void* x, plm_dtype x_dtype, const 
     if (rows == 0 || n == 0) return PLM_OK;
     PLM_CHECK_ARG(x && weight && scale && offsets && y, op, "null pointer");
     PLM_CHECK_ARG(aligned(x, 16) && aligned(weight, 16), op, "x and weight must be 16-byte aligned");
-    const int shape = grouped_shape_for(rows, n_experts);
-    const int64_t max_tiles = ceil_div(rows, grouped_block_rows(shape)) + n_experts;
-    const int64_t need = kCounterBytes + max_tiles * 12;
+    PLM_CHECK_ARG(format == PLM_INT4, op, "grouped GEMMs take int4 experts");
+    const grouped_plan p = plan_grouped(rows, n_experts);
+    const int64_t need = kCounterBytes + p.slots() * 12;
     if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need) {
         set_error(op, "workspace of %lld bytes required, %zu given", static_cast<long long>(need), workspace_bytes);
         return PLM_ERR_WORKSPACE;
     }
     auto* tiles = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + kCounterBytes);
     hipStream_t s = as_stream(stream);
-    if (int rc = launch_tiles(op, offsets, n_experts, grouped_block_rows(shape), max_tiles, tiles, s)) return rc;
-    return launch_grouped(op, format, x, x_dtype == PLM_BF16, weight, scale, scale_dtype, rows, n, k, block_n,
-                          group_size, y, tiles, max_tiles, nullptr, shape, s);
+    if (int rc = launch_tiles(op, offsets, n_experts, p, tiles, s)) return rc;
+    return launch_plan(op, p, x, x_dtype == PLM_BF16, weight, scale, scale_dtype, rows, n, k, block_n, group_size, y,
+                       tiles, nullptr, s);
 }
 
 int64_t plm_grouped_gemm_workspace_bytes(int64_t rows, int64_t n_experts) {
     if (rows <= 0 || n_experts <= 0) return kCounterBytes;
-    const int shape = grouped_shape_for(rows, n_experts);
-    return kCounterBytes + (ceil_div(rows, grouped_block_rows(shape)) + n_experts) * 12;
+    return kCounterBytes + plan_grouped(rows, n_experts).slots() * 12;
 }
 
 int64_t plm_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t n_experts, int64_t hidden,
@@ -278,13 +411,16 @@ int plm_moe(const void* h, plm_dtype dtype, const int32_t* top_experts, const fl
     PLM_CHECK_ARG(group_size > 0 && group_size % 16 == 0 && hidden % group_size == 0 && intermediate % group_size == 0,
                   op, "group_size must be a positive multiple of 16 dividing hidden and intermediate");
     PLM_CHECK_ARG(tokens * top_k <= (int64_t{1} << 30), op, "too many assignments");
+    PLM_CHECK_ARG(hidden % 8 == 0 && intermediate % 8 == 0, op, "hidden and intermediate must be multiples of 8");
+    PLM_CHECK_ARG(aligned(h, 16) && aligned(out, 16) && aligned(workspace, 16), op,
+                  "h, out and workspace must be 16-byte aligned");
     if (tokens == 0) return PLM_OK;
     PLM_CHECK_ARG(h && top_experts && top_weights && gate_up_weight && gate_up_scale && down_weight && down_scale &&
                       offsets && out,
                   op, "null pointer");
     const int64_t rows = tokens * top_k;
-    const int64_t max_tiles = moe_max_tiles(rows, n_experts);
-    const moe_ws l = moe_layout(tokens, top_k, n_experts, hidden, intermediate, max_tiles);
+    const grouped_plan p = plan_grouped(rows, n_experts);
+    const moe_ws l = moe_layout(tokens, top_k, n_experts, hidden, intermediate, p.slots());
     if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < l.total) {
         set_error(op, "workspace of %lld bytes required, %zu given", static_cast<long long>(l.total), workspace_bytes);
         return PLM_ERR_WORKSPACE;
@@ -292,38 +428,38 @@ int plm_moe(const void* h, plm_dtype dtype, const int32_t* top_experts, const fl
     auto* base = static_cast<uint8_t*>(workspace);
     hipStream_t s = as_stream(stream);
     const bool bf16 = dtype == PLM_BF16;
-    const int shape = grouped_shape_for(rows, n_experts);
     auto* tiles = reinterpret_cast<int32_t*>(base + l.tiles);
     if (int rc = launch_sort(op, top_experts, top_weights, rows, top_k, n_experts, base, l, offsets, s)) return rc;
-    if (int rc = launch_tiles(op, offsets, n_experts, grouped_block_rows(shape), max_tiles, tiles, s)) return rc;
+    if (int rc = launch_tiles(op, offsets, n_experts, p, tiles, s)) return rc;
     // gate_up: [rows, 2I] = h[sorted_token] @ gate_up_e^T
-    if (int rc = launch_grouped(op, PLM_INT4, h, bf16, gate_up_weight, gate_up_scale, scale_dtype, rows,
-                                2 * intermediate, hidden, 1, group_size, base + l.gu, tiles, max_tiles,
-                                reinterpret_cast<const int32_t*>(base + l.sorted_token), shape, s))
+    if (int rc = launch_plan(op, p, h, bf16, gate_up_weight, gate_up_scale, scale_dtype, rows, 2 * intermediate,
+                             hidden, 1, group_size, base + l.gu, tiles,
+                             reinterpret_cast<const int32_t*>(base + l.sorted_token), s))
         return rc;
     const int64_t act_n = rows * intermediate;
+    const unsigned act_blocks = static_cast<unsigned>(ceil_div(act_n / 8, 256));
     if (bf16)
-        silu_mul_kernel<true><<<static_cast<unsigned>(ceil_div(act_n, 256)), 256, 0, s>>>(
+        silu_mul_kernel<true><<<act_blocks, 256, 0, s>>>(
             reinterpret_cast<const uint16_t*>(base + l.gu), rows, int(intermediate),
             reinterpret_cast<uint16_t*>(base + l.act));
     else
-        silu_mul_kernel<false><<<static_cast<unsigned>(ceil_div(act_n, 256)), 256, 0, s>>>(
+        silu_mul_kernel<false><<<act_blocks, 256, 0, s>>>(
             reinterpret_cast<const uint16_t*>(base + l.gu), rows, int(intermediate),
             reinterpret_cast<uint16_t*>(base + l.act));
     PLM_HIP_LAUNCH_CHECK(op);
     // down: [rows, H] = act @ down_e^T
-    if (int rc = launch_grouped(op, PLM_INT4, base + l.act, bf16, down_weight, down_scale, scale_dtype, rows, hidden,
-                                intermediate, 1, group_size, base + l.d, tiles, max_tiles, nullptr, shape, s))
+    if (int rc = launch_plan(op, p, base + l.act, bf16, down_weight, down_scale, scale_dtype, rows, hidden,
+                             intermediate, 1, group_size, base + l.d, tiles, nullptr, s))
         return rc;
-    const int64_t out_n = tokens * hidden;
+    const dim3 cgrid(static_cast<unsigned>(tokens), static_cast<unsigned>(ceil_div(hidden / 8, 256)));
     if (bf16)
-        moe_combine_kernel<true><<<static_cast<unsigned>(ceil_div(out_n, 256)), 256, 0, s>>>(
+        moe_combine_kernel<true><<<cgrid, 256, 0, s>>>(
             reinterpret_cast<const uint16_t*>(base + l.d), reinterpret_cast<const int32_t*>(base + l.position),
-            top_weights, tokens, int(top_k), int(hidden), static_cast<uint16_t*>(out));
+            top_weights, int(top_k), int(hidden), static_cast<uint16_t*>(out));
     else
-        moe_combine_kernel<false><<<static_cast<unsigned>(ceil_div(out_n, 256)), 256, 0, s>>>(
+        moe_combine_kernel<false><<<cgrid, 256, 0, s>>>(
             reinterpret_cast<const uint16_t*>(base + l.d), reinterpret_cast<const int32_t*>(base + l.position),
-            top_weights, tokens, int(top_k), int(hidden), static_cast<uint16_t*>(out));
+            top_weights, int(top_k), int(hidden), static_cast<uint16_t*>(out));
     PLM_HIP_LAUNCH_CHECK(op);
     return PLM_OK;
 }
