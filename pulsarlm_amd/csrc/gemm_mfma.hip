@@ -82,8 +82,6 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     constexpr int A_PW = (A_CHUNKS + NW - 1) / NW;  // 1 KiB chunks each wavefront loads per K step
     constexpr int B_PW = (B_CHUNKS + NW - 1) / NW;
     static_assert(A_STAGE % 1024 == 0 && B_STAGE % 1024 == 0, "stages are whole 1 KiB chunks");
-    static_assert((A_CHUNKS % NW == 0 || A_CHUNKS < NW) && (B_CHUNKS % NW == 0 || B_CHUNKS < NW),
-                  "chunks split evenly over the wavefronts that load them");
     constexpr int ST = UNIFORM ? 1 : 4;  // scale values per strip per K step
     constexpr int ES = WIDE ? 4 : 2;     // scale element bytes
 
@@ -174,11 +172,11 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         uint8_t* sa = lds + stage * STAGE;
 #pragma unroll
         for (int i = 0; i < A_PW; ++i)
-            if (A_CHUNKS >= NW || wave < A_CHUNKS)  // wave-uniform
+            if (A_CHUNKS % NW == 0 || wave * A_PW + i < A_CHUNKS)  // wave-uniform
                 buffer_load_lds16(a_rsrc, sa + (wave * A_PW + i) * 1024, a_offset(i, kt), kt * ARB);
 #pragma unroll
         for (int i = 0; i < B_PW; ++i)
-            if (B_CHUNKS >= NW || wave < B_CHUNKS)  // wave-uniform
+            if (B_CHUNKS % NW == 0 || wave * B_PW + i < B_CHUNKS)  // wave-uniform
                 buffer_load_lds16(b_rsrc, sa + A_STAGE + (wave * B_PW + i) * 1024, b_off[i], kt * TB);
     };
 
@@ -351,6 +349,7 @@ struct shape {
     constexpr int bs() const { return wn * ns; }
 };
 constexpr shape kHuge{2, 4, 8, 4};   // 256 x 256, 8 wavefronts (int4 only: two stages fill the 160 KiB LDS)
+constexpr shape kWide{2, 4, 8, 3};   // 256 x 192, 8 wavefronts (int4 only; N = 6144 gives whole rounds)
 constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts
 constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
 // Grouped calls also use short row blocks for experts with few rows.
@@ -358,15 +357,15 @@ constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
 constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
 constexpr shape kGroupedShapes[5] = {kRows16, kRows64, kSmall, kLarge, kHuge};
 constexpr shape shape_of(int id) {
-    return id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
+    return id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
 }
 // Relative MFMA throughput per unit of tile area, measured on MI355X at the Qwen3-8B shapes.
-constexpr double kShapeRate[5] = {0.75, 0.7, 1.0, 0.65, 0.3};
+constexpr double kShapeRate[6] = {0.75, 0.7, 1.0, 0.65, 0.3, 0.95};
 
 }  // namespace
 
 struct mfma_config {
-    int shape;  // 0 small, 1 large, 2 huge, 3 rows64, 4 rows16
+    int shape;  // 0 small, 1 large, 2 huge, 3 rows64, 4 rows16, 5 wide
     int m_blocks, n_blocks;
     int splits, tiles_per_split;
 };
@@ -397,12 +396,12 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
         return static_cast<double>(rounds) * (c.tiles_per_split + 3) * sh.bm() * sh.bs() / kShapeRate[c.shape];
     };
     if (const char* env = getenv("PLM_MFMA")) {  // tuning sweeps: S, L, H or R
-        const int id = env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : 0;
-        return config(id == 2 && f != PLM_INT4 ? 1 : id);
+        const int id = env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
+        return config((id == 2 || id == 5) && f != PLM_INT4 ? 1 : id);
     }
     mfma_config best = config(0);
-    for (int id = 1; id < 4; ++id) {
-        if (id == 2 && f != PLM_INT4) continue;
+    for (int id : {1, 2, 3, 5}) {
+        if ((id == 2 || id == 5) && f != PLM_INT4) continue;
         const mfma_config c = config(id);
         if (cost(c) < cost(best)) best = c;
     }
@@ -424,6 +423,11 @@ void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
         if (shape == 2) {
             mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kHuge.wm, kHuge.wn, kHuge.mt, kHuge.ns>
                 <<<grid, kHuge.wm * kHuge.wn * 64, 0, s>>>(a);
+            return;
+        }
+        if (shape == 5) {
+            mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kWide.wm, kWide.wn, kWide.mt, kWide.ns>
+                <<<grid, kWide.wm * kWide.wn * 64, 0, s>>>(a);
             return;
         }
     }
