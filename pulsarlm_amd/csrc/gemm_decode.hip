@@ -3,7 +3,15 @@
 // Counterpart of the reference's marlin_kernel at tile_m = 16 (pulsarlm-core/src/kernels/
 // marlin.cu:251-389, dispatched for M <= 16 at :577-596) together with its split-K
 // partial sum and combine (pulsarlm-core/inc/pulsarlm/kernels/dequant_gemm_common.cuh:
-// 56-133). Designed for gfx950 rather than translated:
+// 56-133). Designed for gfx950 rather than translated. Two kernels:
+//
+// decode_rr_kernel (scale groups a power-of-two multiple of 128, x fits in LDS, one load
+// batch per wavefront): a workgroup owns whole strips over all of K, its wavefronts take
+// K tiles round-robin, x and scales are staged per wavefront in LDS, weights stream with
+// the nontemporal policy; see its own comment. Measured on MI355X it beats the kernel
+// below at every Qwen3-8B shape except K = 12288, where a wavefront would hold 6 tiles.
+//
+// decode_kernel (every other case, including W8A8 and groups smaller than 128):
 //
 // * A wavefront owns SP 16-column strips over TPW consecutive 128-wide K tiles. Each
 //   lane issues one 16-byte load per int4 tile (two per fp8 tile), so a wavefront's
@@ -18,6 +26,8 @@
 // * The NW wavefronts of a workgroup cover NW * TPW K tiles and reduce through LDS in a
 //   fixed order; K splits across workgroups write fp32 partials and the last workgroup
 //   to arrive at a column block sums them in split order, so results are deterministic.
+#include <algorithm>
+
 #include "plm_common.hpp"
 
 namespace plm {
@@ -109,7 +119,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
 #pragma unroll
             for (int j = 0; j < SP; ++j) {
 #pragma unroll
-                for (int h = 0; h < TB / 1024; ++h) b.w[tt][j][h] = buffer_load16(wr[j], w_lane + h * 1024, w_off);
+                for (int h = 0; h < TB / 1024; ++h) b.w[tt][j][h] = buffer_load16_stream(wr[j], w_lane + h * 1024, w_off);
                 if constexpr (UNIFORM) {
                     const int s_off = ok ? (kt * kTileK / a.group_size) * a.scale_cols * ES : kOOB;
                     if constexpr (WIDE) b.s[tt][j] = buffer_load_u32(sr[j], s_lane, s_off);
@@ -290,6 +300,175 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Round-robin decode kernel (M <= 4, scale groups a power-of-two multiple of 128).
+//
+// A workgroup owns SG strips over the whole of K, so no K split crosses workgroups and
+// nothing waits on another workgroup. Its NW wavefronts take the K tiles round-robin
+// (wavefront w takes tiles w, w + NW, ...): at each load step the workgroup's loads of a
+// strip cover NW consecutive KiB. Each wavefront first copies into its own LDS area, with
+// buffer loads to LDS, the x rows (< M) and the scales of its tiles (a few instructions
+// instead of one scale load per tile); all address math is shifts and masks, so the
+// weight loads issue right after. Weights are dequantized exactly (round(q * round(s)))
+// into the MFMA operand; the wavefronts' partial sums are added through LDS in wavefront
+// order and the workgroup stores y.
+//
+// SC: scale layout per (strip, group): 0 = 16 x 16-bit, 1 = 16 x fp32, 2 = 1 x fp32.
+// ---------------------------------------------------------------------------
+struct rr_args {
+    const uint16_t* x;
+    const uint8_t* w;
+    const uint8_t* scale;
+    uint16_t* y;
+    int m, n, k;
+    int ktiles, strips, groups;
+    int tpg_shift;    // log2(group_size / 128)
+    int nkt_shift;    // log2 of the per-wavefront tile slots (a power of two >= ceil(ktiles / NW))
+    int x_bytes;      // per-wavefront x area: M rows x slots x 256 B, rounded to 1 KiB
+    int wave_bytes;   // per-wavefront LDS area (x, then scales)
+    int scale_dtype;
+};
+
+template <int SC> struct rr_scale {
+    static constexpr int eb = SC == 0 ? 32 : (SC == 1 ? 64 : 4);  // bytes per (strip, group)
+    static constexpr int cs = eb < 16 ? eb : 16;                   // bytes per lane per copy
+    static constexpr int parts_shift = SC == 0 ? 1 : (SC == 1 ? 2 : 0);
+};
+
+template <plm_format F, bool BF16, int SG, int NW, int CH, int SC>
+__global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
+    constexpr int TB = fmt_traits<F>::tile_bytes;
+    constexpr int NL = TB / 1024;  // 16-byte loads per lane per tile
+    constexpr int EB = rr_scale<SC>::eb, CS = rr_scale<SC>::cs, PS = rr_scale<SC>::parts_shift;
+    constexpr bool WIDE = SC != 0;
+    const int lane = threadIdx.x & 63;
+    const int wave = uniform(threadIdx.x >> 6);
+    const int col16 = lane & 15;
+    const int kq = lane >> 4;
+    const int strip0 = blockIdx.x * SG;
+    const int nkt_w = (a.ktiles - wave + NW - 1) / NW;  // this wavefront's tiles
+    const int slots = 1 << a.nkt_shift;
+    const bool bf16_scale = a.scale_dtype == PLM_BF16;
+
+    extern __shared__ __attribute__((aligned(16))) uint8_t rr_lds[];
+    uint8_t* xs = rr_lds + wave * a.wave_bytes;
+    uint8_t* ss = xs + a.x_bytes;
+
+    // x: 16-byte chunk j = (row, slot i, column o), LDS [row][slot][256 B].
+    {
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, static_cast<uint32_t>(a.m) * a.k * 2);
+        const int total = a.m << (a.nkt_shift + 4);
+        for (int c = 0; c * 64 < total; ++c) {  // wave-uniform
+            const int j = c * 64 + lane;
+            const int o = j & 15, i = (j >> 4) & (slots - 1), row = j >> (a.nkt_shift + 4);
+            const int kb = ((wave + NW * i) << 8) + (o << 4);  // byte offset in the row
+            const int off = (row < a.m && i < nkt_w && kb < a.k * 2) ? row * a.k * 2 + kb : kOOB;
+            buffer_load_lds16(xr, xs + c * 1024, off, 0);
+        }
+    }
+    // Scales: entry (strip sj, slot i) of EB bytes, LDS [sj][slot][EB], CS bytes per lane.
+    {
+        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.scale, static_cast<uint32_t>(a.strips) * a.groups * EB);
+        const int total = (SG << a.nkt_shift) << PS;
+        for (int c = 0; c * 64 < total; ++c) {  // wave-uniform
+            const int j = c * 64 + lane;
+            const int e = j >> PS, p = j & ((1 << PS) - 1);
+            const int sj = e >> a.nkt_shift, i = e & (slots - 1);
+            const int st = min(strip0 + sj, a.strips - 1);
+            const int g = (wave + NW * i) >> a.tpg_shift;
+            const int off = (sj < SG && i < nkt_w) ? (st * a.groups + g) * EB + p * CS : kOOB;
+            auto* dst = (__attribute__((address_space(3))) void*)(ss + c * 64 * CS);
+            if constexpr (CS == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, dst, 16, off, 0, 0, 0);
+            else __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, dst, 4, off, 0, 0, 0);
+        }
+    }
+    asm volatile("" ::: "memory");  // the weight loads below are issued after the staging copies
+
+    __amdgpu_buffer_rsrc_t wr[SG];
+#pragma unroll
+    for (int sj = 0; sj < SG; ++sj) {
+        const int st = min(strip0 + sj, a.strips - 1);
+        wr[sj] = make_rsrc(a.w + static_cast<int64_t>(st) * a.ktiles * TB, static_cast<uint32_t>(a.ktiles) * TB);
+    }
+    const int w_lane = lane * 16;
+
+    f32x4_t acc[SG];
+#pragma unroll
+    for (int sj = 0; sj < SG; ++sj) acc[sj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int xrow = min(col16, a.m - 1);
+    for (int i0 = 0; i0 < nkt_w; i0 += CH) {  // wave-uniform
+        u32x4_t wv[CH][SG][NL];
+#pragma unroll
+        for (int ii = 0; ii < CH; ++ii) {
+            const int i = i0 + ii;
+            const int w_off = i < nkt_w ? (wave + NW * i) * TB : kOOB;
+#pragma unroll
+            for (int sj = 0; sj < SG; ++sj)
+#pragma unroll
+                for (int h = 0; h < NL; ++h) wv[ii][sj][h] = buffer_load16_stream(wr[sj], w_lane + h * 1024, w_off);
+        }
+        if (i0 == 0) {
+            // The staging copies were issued before these loads: once only the weight loads
+            // are outstanding, the wavefront's x and scales are in LDS.
+            constexpr int kLoads = CH * SG * NL;
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");
+        }
+#pragma unroll
+        for (int ii = 0; ii < CH; ++ii) {
+            const int i = i0 + ii;
+            if (i >= nkt_w) break;  // wave-uniform
+            u32x4_t xf[4];
+            const uint8_t* xp = xs + (((xrow << a.nkt_shift) + i) << 8) + kq * 16;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xf[t] = *reinterpret_cast<const u32x4_t*>(xp + 64 * t);
+#pragma unroll
+            for (int sj = 0; sj < SG; ++sj) {
+                const uint8_t* sp = ss + (((sj << a.nkt_shift) + i) * EB) + (SC == 2 ? 0 : col16 * (WIDE ? 4 : 2));
+                const uint32_t bits = WIDE ? *reinterpret_cast<const uint32_t*>(sp)
+                                           : static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(sp));
+                const float raw = scale_from_bits<WIDE>(bits, bf16_scale);
+                if constexpr (F == PLM_INT4) {
+                    const int4_scale k4 = make_int4_scale<BF16>(raw);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        acc[sj] = mfma16x16x32<BF16>(xf[t], dq_int4<BF16>(wv[ii][sj][0][t], k4), acc[sj]);
+                } else {
+                    const float sc = round_to<BF16>(raw);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const u32x4_t& v = wv[ii][sj][t >> 1];
+                        acc[sj] = mfma16x16x32<BF16>(xf[t], dq_fp8<BF16>(v[(t & 1) * 2], v[(t & 1) * 2 + 1], sc), acc[sj]);
+                    }
+                }
+            }
+        }
+    }
+
+    // Partial sums through LDS, over the staging areas once every wavefront is done with
+    // them: red[sj][wave][lane < 16 RQ][4], rows 4 (lane / 16) + i of column lane % 16.
+    const int rq = (a.m + 3) >> 2;
+    float* red = reinterpret_cast<float*>(rr_lds);
+    __syncthreads();
+    if (lane < 16 * rq) {
+#pragma unroll
+        for (int sj = 0; sj < SG; ++sj)
+            *reinterpret_cast<f32x4_t*>(red + (((sj * NW + wave) << 6) + lane) * 4) = acc[sj];
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < SG * 256; e += NW * 64) {
+        const int c = e & 15, row = (e >> 4) & 15, sj = e >> 8;
+        const int col = (strip0 + sj) * kTileN + c;
+        if (row < a.m && col < a.n) {
+            const int ln = c + 16 * (row >> 2), i = row & 3;
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) v += red[(((sj * NW + w) << 6) + ln) * 4 + i];
+            a.y[static_cast<int64_t>(row) * a.n + col] = static_cast<uint16_t>(to_bits16<BF16>(v));
+        }
+    }
+}
+
 }  // namespace
 
 struct decode_config {
@@ -403,6 +582,69 @@ void launch_decode_f(const decode_args& a, const decode_config& c, bool uniform,
 }
 }  // namespace
 
+namespace {
+template <plm_format F, bool BF16, int SG, int NW, int CH>
+void launch_rr_t(const rr_args& a, int sc, int grid, size_t lds, hipStream_t s) {
+    if (sc == 0) decode_rr_kernel<F, BF16, SG, NW, CH, 0><<<grid, NW * 64, lds, s>>>(a);
+    else if (sc == 1) decode_rr_kernel<F, BF16, SG, NW, CH, 1><<<grid, NW * 64, lds, s>>>(a);
+    else decode_rr_kernel<F, BF16, SG, NW, CH, 2><<<grid, NW * 64, lds, s>>>(a);
+}
+template <plm_format F, bool BF16, int NW, int CH>
+void launch_rr_sg(const rr_args& a, int sc, int sg, size_t lds, hipStream_t s) {
+    const int grid = static_cast<int>(ceil_div(a.strips, sg));
+    switch (sg) {
+        case 1: launch_rr_t<F, BF16, 1, NW, CH>(a, sc, grid, lds, s); break;
+        case 2: launch_rr_t<F, BF16, 2, NW, CH>(a, sc, grid, lds, s); break;
+        case 3: launch_rr_t<F, BF16, 3, NW, CH>(a, sc, grid, lds, s); break;
+        default:
+            // fp8 tiles take twice the registers: at most three strips.
+            if constexpr (F == PLM_FP8) launch_rr_t<F, BF16, 3, NW, CH>(a, sc, static_cast<int>(ceil_div(a.strips, 3)), lds, s);
+            else if (sg == 4) launch_rr_t<F, BF16, 4, NW, CH>(a, sc, grid, lds, s);
+            else launch_rr_t<F, BF16, 6, NW, CH>(a, sc, grid, lds, s);
+            break;
+    }
+}
+}  // namespace
+
+struct rr_config {
+    int sg = 0, nw = 0;  // sg == 0: not applicable
+};
+
+// Round-robin kernel choice (measured on MI355X at the Qwen3-8B shapes). M <= 4: one
+// strip per workgroup, 16 wavefronts, or 8 when the strips alone give every CU four
+// workgroups. M > 4 (x fills most of LDS, one workgroup per CU): strips grouped so that
+// there is about one workgroup per CU.
+rr_config choose_rr(int64_t m, int64_t n, int64_t k) {
+    rr_config c;
+    if (m > 16) return c;
+    const int64_t strips = ceil_div(n, kTileN);
+    const int64_t cus = cu_count();
+    c.sg = 1;
+    c.nw = 16;
+    if (m <= 4) {
+        if (strips >= 4 * cus) c.nw = 8;
+    } else {
+        c.sg = 6;
+        for (int sg : {1, 2, 3, 4}) {
+            if (sg * cus >= strips) {
+                c.sg = sg;
+                break;
+            }
+        }
+    }
+    if (const char* env = getenv("PLM_DECODE_RR")) {  // "sg,nw" for tuning sweeps; "0" disables
+        int sg = 0, nw = 0;
+        const int got = sscanf(env, "%d,%d", &sg, &nw);
+        if (got >= 1 && sg == 0) return rr_config{};
+        if (got == 2 && (sg == 1 || sg == 2 || sg == 3 || sg == 4 || sg == 6) && (nw == 8 || nw == 16)) {
+            c.sg = sg;
+            c.nw = nw;
+        }
+    }
+    (void)k;
+    return c;
+}
+
 // x rows are staged in LDS for M up to this (above it the 16-byte loads of x are mostly full).
 constexpr int64_t kStageMaxM = 4;
 constexpr int64_t kStageMaxBytes = 96 * 1024;  // staging area per workgroup
@@ -453,6 +695,62 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
         a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     }
     const bool uniform = group_size % kTileK == 0;
+    const int64_t tpg = group_size / kTileK;
+    const int sc_mode = d.scale_cols == 16 ? (scale_dtype == PLM_FP32 ? 1 : 0) : (scale_dtype == PLM_FP32 ? 2 : -1);
+    if (uniform && (tpg & (tpg - 1)) == 0 && xq == nullptr && sc_mode >= 0 && !no_x_staging()) {
+        const rr_config rc = choose_rr(m, n, k);
+        if (rc.sg > 0) {
+            rr_args r{};
+            r.x = static_cast<const uint16_t*>(x);
+            r.w = static_cast<const uint8_t*>(w);
+            r.scale = static_cast<const uint8_t*>(scale);
+            r.y = static_cast<uint16_t*>(y);
+            r.m = static_cast<int>(m);
+            r.n = static_cast<int>(n);
+            r.k = static_cast<int>(k);
+            r.ktiles = static_cast<int>(d.ktiles);
+            r.strips = static_cast<int>(d.strips);
+            r.groups = static_cast<int>(d.groups);
+            r.scale_dtype = scale_dtype;
+            while ((int64_t{1} << r.tpg_shift) < tpg) ++r.tpg_shift;
+            const int64_t nkt = ceil_div(d.ktiles, rc.nw);
+            while ((int64_t{1} << r.nkt_shift) < nkt) ++r.nkt_shift;
+            const int64_t slots = int64_t{1} << r.nkt_shift;
+            const int eb = sc_mode == 0 ? 32 : (sc_mode == 1 ? 64 : 4);
+            r.x_bytes = static_cast<int>(round_up(m * slots * 256, 1024));
+            // Scale copies write whole instructions: 64 lanes x (16 or 4) bytes.
+            const int64_t cs = eb < 16 ? eb : 16;
+            const int64_t s_bytes = round_up(rc.sg * slots * eb, 64 * cs);
+            r.wave_bytes = static_cast<int>(r.x_bytes + s_bytes);
+            const int64_t red = int64_t{rc.sg} * rc.nw * 64 * 16;
+            const int64_t lds = std::max<int64_t>(int64_t{rc.nw} * r.wave_bytes, red);
+            // One batch of loads per wavefront (CH tiles) keeps every load in flight at once.
+            const int64_t ch = rc.nw == 16 ? 2 : (f == PLM_INT4 ? 4 : 2);
+            if (lds <= 160 * 1024 && slots <= ch) {
+                const size_t l = static_cast<size_t>(lds);
+                // CH: tiles per load batch (all of a wavefront's tiles at K = 4096).
+                if (f == PLM_INT4) {
+                    if (rc.nw == 16) {
+                        if (bf16) launch_rr_sg<PLM_INT4, true, 16, 2>(r, sc_mode, rc.sg, l, s);
+                        else launch_rr_sg<PLM_INT4, false, 16, 2>(r, sc_mode, rc.sg, l, s);
+                    } else {
+                        if (bf16) launch_rr_sg<PLM_INT4, true, 8, 4>(r, sc_mode, rc.sg, l, s);
+                        else launch_rr_sg<PLM_INT4, false, 8, 4>(r, sc_mode, rc.sg, l, s);
+                    }
+                } else {
+                    if (rc.nw == 16) {
+                        if (bf16) launch_rr_sg<PLM_FP8, true, 16, 2>(r, sc_mode, rc.sg, l, s);
+                        else launch_rr_sg<PLM_FP8, false, 16, 2>(r, sc_mode, rc.sg, l, s);
+                    } else {
+                        if (bf16) launch_rr_sg<PLM_FP8, true, 8, 2>(r, sc_mode, rc.sg, l, s);
+                        else launch_rr_sg<PLM_FP8, false, 8, 2>(r, sc_mode, rc.sg, l, s);
+                    }
+                }
+                PLM_HIP_LAUNCH_CHECK(op);
+                return PLM_OK;
+            }
+        }
+    }
     if (f == PLM_INT4) {
         if (bf16) launch_decode_f<PLM_INT4, true>(a, c, uniform, s);
         else launch_decode_f<PLM_INT4, false>(a, c, uniform, s);

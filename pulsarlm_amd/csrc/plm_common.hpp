@@ -232,6 +232,13 @@ __device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t r, int o
 __device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
     return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
 }
+#ifndef PLM_STREAM_POLICY
+#define PLM_STREAM_POLICY 2
+#endif
+// Streaming (read-once) weights: the nontemporal policy (nt).
+__device__ __forceinline__ u32x4_t buffer_load16_stream(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, PLM_STREAM_POLICY));
+}
 __device__ __forceinline__ uint32_t buffer_load_u16(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, voffset, soffset, 0);
 }

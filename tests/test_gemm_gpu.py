@@ -132,6 +132,34 @@ def test_int4_gemm_group_sizes(m, g):
     assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, g), None), f"m={m} g={g}")
 
 
+@pytest.mark.parametrize("m", [1, 3, 4, 8, 13, 16])
+@pytest.mark.parametrize("case", ["fp16s-bf16x", "fp32s-bf16x", "bf16s-fp16x", "fp32s-strip", "g256"])
+def test_decode_kernel_variants(m, case):
+    """The M <= 16 decode kernels across scale layouts, activation dtypes and a ragged strip
+    count (N = 8200: 513 strips, so strip groups of 2, 3 or more end in a partial group)."""
+    n, k, g, block_n, dtype = 8200, 512, 128, 1, "bf16"
+    sdt = np.float16
+    if case == "fp32s-bf16x":
+        sdt = np.float32
+    elif case == "bf16s-fp16x":
+        dtype, sdt = "fp16", np.float32
+    elif case == "fp32s-strip":
+        block_n, sdt = 128, np.float32
+    elif case == "g256":
+        g = 256
+    packed, s = int4_case(n, k, g, block_n, seed=m + 7)
+    s = s.astype(sdt)
+    if case == "bf16s-fp16x":  # bf16-stored scales
+        s = O.round_to(s.astype(np.float32), "bf16")
+        s_dev = to_dev(s).to(torch.bfloat16)
+    else:
+        s_dev = scale_tensor(s)
+    w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), s_dev, block_n, g)
+    x = x_case(m, k, dtype, seed=m)
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, TDT[dtype]), w, sc, n, block_n, g)
+    assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, block_n, g, dtype), None), f"{case} m={m}")
+
+
 def test_config1_m16_k4096_n4096():
     """benchmark config 1: M=16, K=N=4096, int4 g128 symmetric, fp16 scales |N(0,.02)|+1e-3."""
     x, packed, s = O.make_w4a16(16, 4096, 4096, 128, seed=1)
