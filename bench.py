@@ -350,7 +350,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "decode_kernel (plm_gemm, M <= 16)",
+            "kernel": "decode_rr_kernel / decode_kernel (plm_gemm, M <= 16)",
             "algorithmic_bytes_per_launch": int(d["per_launch_bytes"]),
             "avg_launch_us": round(d["avg_launch_s"] * 1e6, 3),
         },
