@@ -12,7 +12,9 @@
 //   each owning MT x NS tiles of v_mfma_f32_16x16x32 (bf16/fp16) -- 128 x 64 per
 //   wavefront in the large configuration (256 x 128 per workgroup, one wavefront per
 //   SIMD with the full 512 registers), so each dequantized weight feeds 8 MFMAs and the
-//   dequant VALU work is about half the MFMA time, interleaved with it.
+//   dequant VALU work is about half the MFMA time, interleaved with it. The int4 256 x 256
+//   tile for plain calls uses 8 wavefronts of 256 x 32 each, so every strip is dequantized
+//   by one wavefront only (a 2 x 4 wavefront grid would dequantize each strip twice).
 // * The x tile and the packed weight tiles (1 KiB int4 / 2 KiB fp8 per 16-column strip,
 //   copied verbatim from the plm layout) go from HBM straight into LDS with buffer loads to
 //   LDS (no register staging), double-buffered: the next K step's loads land in one stage
@@ -349,7 +351,9 @@ struct shape {
     constexpr int bs() const { return wn * ns; }
 };
 constexpr shape kHuge{2, 4, 8, 4};   // 256 x 256, 8 wavefronts (int4 only: two stages fill the 160 KiB LDS)
+                                     // (grouped calls; plain calls use kTall, measured 3 % faster)
 constexpr shape kWide{2, 4, 8, 3};   // 256 x 192, 8 wavefronts (int4 only; N = 6144 gives whole rounds)
+constexpr shape kTall{1, 8, 16, 2};  // 256 x 256, 8 wavefronts of 256 x 32 (int4 only): each strip dequantized once
 constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts
 constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
 // Grouped calls also use short row blocks for experts with few rows.
@@ -357,22 +361,22 @@ constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
 constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
 constexpr shape kGroupedShapes[5] = {kRows16, kRows64, kSmall, kLarge, kHuge};
 constexpr shape shape_of(int id) {
-    return id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
+    return id == 6 ? kTall : id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
 }
 // Relative MFMA throughput per unit of tile area, measured on MI355X at the Qwen3-8B shapes.
-constexpr double kShapeRate[6] = {0.75, 0.7, 1.0, 0.65, 0.3, 0.95};
+constexpr double kShapeRate[7] = {0.75, 0.7, 1.0, 0.65, 0.3, 0.95, 1.03};
 
 }  // namespace
 
 struct mfma_config {
-    int shape;  // 0 small, 1 large, 2 huge, 3 rows64, 4 rows16, 5 wide
+    int shape;  // 0 small, 1 large, 2 huge, 3 rows64, 4 rows16, 5 wide, 6 tall
     int m_blocks, n_blocks;
     int splits, tiles_per_split;
 };
 
 // Tile shape and split count: the candidate with the least estimated time, counting whole
-// rounds of workgroups over the CUs and a fixed cost of about three K tiles per workgroup
-// (pipeline fill, epilogue, split-K reduction).
+// rounds of workgroups over the CUs, a fixed cost of about three K tiles per workgroup
+// (pipeline fill, epilogue) and half a K tile per split for the split-K reduction.
 mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
     const int64_t cus = cu_count();
     const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
@@ -393,15 +397,17 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
     auto cost = [&](const mfma_config& c) {
         const shape sh = shape_of(c.shape);
         const int64_t rounds = ceil_div(static_cast<int64_t>(c.m_blocks) * c.n_blocks * c.splits, cus);
-        return static_cast<double>(rounds) * (c.tiles_per_split + 3) * sh.bm() * sh.bs() / kShapeRate[c.shape];
+        // The last workgroup of a split tile reads every split's partials: half a K tile each.
+        const double reduce = c.splits > 1 ? 0.5 * c.splits : 0.0;
+        return static_cast<double>(rounds) * (c.tiles_per_split + 3 + reduce) * sh.bm() * sh.bs() / kShapeRate[c.shape];
     };
     if (const char* env = getenv("PLM_MFMA")) {  // tuning sweeps: S, L, H or R
-        const int id = env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
-        return config((id == 2 || id == 5) && f != PLM_INT4 ? 1 : id);
+        const int id = env[0] == 'X' ? 6 : env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
+        return config((id == 2 || id >= 5) && f != PLM_INT4 ? 1 : id);
     }
     mfma_config best = config(0);
-    for (int id : {1, 2, 3, 5}) {
-        if ((id == 2 || id == 5) && f != PLM_INT4) continue;
+    for (int id : {1, 2, 3, 5, 6}) {
+        if ((id == 2 || id >= 5) && f != PLM_INT4) continue;
         const mfma_config c = config(id);
         if (cost(c) < cost(best)) best = c;
     }
@@ -428,6 +434,11 @@ void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
         if (shape == 5) {
             mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kWide.wm, kWide.wn, kWide.mt, kWide.ns>
                 <<<grid, kWide.wm * kWide.wn * 64, 0, s>>>(a);
+            return;
+        }
+        if (shape == 6) {
+            mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kTall.wm, kTall.wn, kTall.mt, kTall.ns>
+                <<<grid, kTall.wm * kTall.wn * 64, 0, s>>>(a);
             return;
         }
     }
