@@ -184,6 +184,26 @@ int plm_moe(const void* h, plm_dtype dtype, const int32_t* top_experts, const fl
             const void* down_weight, const void* down_scale, plm_dtype scale_dtype, int64_t group_size,
             int32_t* offsets, void* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Router: for each token t, the softmax in fp32 of its logits row (rows row_stride
+ * elements apart, dtype PLM_FP32, PLM_FP16 or PLM_BF16), its k most probable experts in
+ * descending order (the lower expert first among equal probabilities) and their
+ * probabilities divided by their sum: weights fp32 [tokens, k]; the experts as int64
+ * [tokens, k] into `chosen` and/or as int32 into `chosen_i32` (what plm_moe takes),
+ * either may be NULL. experts <= 4096, 1 <= k <= min(experts, 64).
+ * Replaces route_top_k_cuda (pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:37-40,
+ * pulsarlm-core/src/kernels/moe_routing.cu:56-110,137-166).
+ */
+int plm_route_top_k(const void* logits, plm_dtype dtype, int64_t tokens, int64_t experts, int64_t row_stride,
+                    int64_t k, float* weights, int64_t* chosen, int32_t* chosen_i32, void* stream);
+
+/*
+ * y [tokens, n] = round(round(silu(g)) * u) for contiguous x [tokens, 2n] = [g | u],
+ * silu(g) = g / (1 + exp(-g)) in fp32, round = to dtype (PLM_FP32, PLM_FP16, PLM_BF16).
+ * Replaces silu_mul_cuda (ops.hpp:42-43, moe_routing.cu:112-131,168-192).
+ */
+int plm_silu_mul(const void* x, plm_dtype dtype, int64_t tokens, int64_t n, void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

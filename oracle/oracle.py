@@ -25,7 +25,9 @@ path in pulsarlm-core:
   (``pulsarlm-core/src/kernels/int4_gemm.cu:136-138``);
 * the MoE ``routed_experts`` algorithm (``pulsarlm-core/src/engine/model/
   paged_forward.cpp:108-130``) and the per-expert dense restatement of
-  ``pulsarlm-core/tests/model/test_qwen3_5_moe.cpp:229-248``.
+  ``pulsarlm-core/tests/model/test_qwen3_5_moe.cpp:229-248``;
+* the router ``route_top_k`` and the activation ``silu_mul``
+  (``pulsarlm-core/src/kernels/moe_routing.cu:56-131``).
 
 How each function is pinned (checks live in ``tests/test_oracle.py``):
 
@@ -42,6 +44,10 @@ How each function is pinned (checks live in ``tests/test_oracle.py``):
 * ``routed_experts_ref``: against the per-expert dense restatement.
 * ``fp8_block_quantize``: invariants (one code per block at |448|, exact
   reconstruction bound) and against torch's e4m3 cast.
+* ``route_top_k_ref``: torch's softmax and topk (the reference test's own checks,
+  ``pulsarlm-core/tests/kernels/test_fused_ops.cpp:83-100``) and hand-derived
+  tie-breaking cases.
+* ``silu_mul_ref``: torch's silu on a sweep, and the closed forms at 0 and large |g|.
 * ``quantize_per_token_e4m3`` (W8A8 mode): parity unpinned by the reference,
   which has no fp8-activation path; checked only against torch's e4m3 cast.
 """
@@ -518,3 +524,35 @@ def plm_layout_scale(scale, n: int, k: int, block_n: int, group_size: int) -> np
         ok = col < n
         out[ok, : k // group_size, c] = s[col[ok] // block_n]
     return out
+
+
+# ---------------------------------------------------------------------------
+# MoE router and activation (pulsarlm-core/src/kernels/moe_routing.cu)
+# ---------------------------------------------------------------------------
+
+
+def route_top_k_ref(logits, k: int):
+    """route_top_k (moe_routing.cu:56-110): the softmax of each row in fp32, its k most
+    probable experts in descending order with the lower expert first among equal
+    probabilities (int64 [T, k]), and their probabilities divided by their sum, taken
+    in that order (fp32 [T, k]). Returns (weights, experts, probabilities)."""
+    x = np.asarray(logits, dtype=np.float32)
+    shifted = np.exp(x - x.max(axis=1, keepdims=True)).astype(np.float32)
+    p = (shifted / shifted.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    idx = np.broadcast_to(np.arange(x.shape[1]), p.shape)
+    order = np.lexsort((idx, -p), axis=-1)
+    experts = order[:, :k].astype(np.int64)
+    top = np.take_along_axis(p, experts, axis=1)
+    total = np.cumsum(top, axis=1, dtype=np.float32)[:, -1:]
+    return (top / total).astype(np.float32), experts, p
+
+
+def silu_mul_ref(x, dtype: str = "bf16") -> np.ndarray:
+    """silu_mul (moe_routing.cu:112-131): round(round(silu(g)) * u) for x = [g | u] per
+    row, silu(g) = g / (1 + exp(-g)) in fp32, round = to ``dtype`` ("fp32": none)."""
+    x = np.asarray(x, dtype=np.float32)
+    n = x.shape[1] // 2
+    g, u = x[:, :n], x[:, n:]
+    rnd = (lambda v: np.asarray(v, dtype=np.float32)) if dtype == "fp32" else (lambda v: round_to(v, dtype))
+    act = rnd((g / (np.float32(1) + np.exp(-g))).astype(np.float32))
+    return rnd((act * u).astype(np.float32))

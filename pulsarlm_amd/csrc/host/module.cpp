@@ -18,6 +18,8 @@ PYBIND11_MODULE(_host, m) {
     m.def("repack_int4_experts_cuda", &pulsarlm::repack_int4_experts_cuda);
     m.def("grouped_gemm_int4_cuda", &pulsarlm::grouped_gemm_int4_cuda);
     m.def("routed_experts_int4_cuda", &pulsarlm::routed_experts_int4_cuda);
+    m.def("route_top_k_cuda", &pulsarlm::route_top_k_cuda);
+    m.def("silu_mul_cuda", &pulsarlm::silu_mul_cuda);
     py::class_<pulsarlm::linear>(m, "linear")
         .def_static("dense", &pulsarlm::linear::dense)
         .def_static("fp8", &pulsarlm::linear::fp8)

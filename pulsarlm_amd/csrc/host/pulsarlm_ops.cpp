@@ -263,4 +263,29 @@ std::tuple<at::Tensor, at::Tensor> routed_experts_int4_cuda(const at::Tensor& h,
     return {out, offsets};
 }
 
+std::tuple<at::Tensor, at::Tensor> route_top_k_cuda(const at::Tensor& logits, int64_t k) {
+    const char* op = "route_top_k";
+    TORCH_CHECK(logits.is_cuda() && logits.dim() == 2 && logits.stride(1) == 1, op,
+                ": logits must be CUDA [tokens, experts], each row contiguous");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(logits.device());
+    const int64_t tokens = logits.size(0), experts = logits.size(1);
+    at::Tensor weights = at::empty({tokens, k}, logits.options().dtype(at::kFloat));
+    at::Tensor chosen = at::empty({tokens, k}, logits.options().dtype(at::kLong));
+    check_rc(plm_route_top_k(logits.data_ptr(), dtype_of(op, logits.scalar_type()), tokens, experts,
+                             tokens > 1 ? logits.stride(0) : experts, k, static_cast<float*>(weights.data_ptr()),
+                             static_cast<int64_t*>(chosen.data_ptr()), nullptr, stream_of(logits)));
+    return {weights, chosen};
+}
+
+at::Tensor silu_mul_cuda(const at::Tensor& x) {
+    const char* op = "silu_mul";
+    TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.is_contiguous() && x.size(1) % 2 == 0, op,
+                ": x must be contiguous CUDA [tokens, 2 * n]");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    const int64_t tokens = x.size(0), n = x.size(1) / 2;
+    at::Tensor y = at::empty({tokens, n}, x.options());
+    check_rc(plm_silu_mul(x.data_ptr(), dtype_of(op, x.scalar_type()), tokens, n, y.data_ptr(), stream_of(x)));
+    return y;
+}
+
 }  // namespace pulsarlm

@@ -73,4 +73,11 @@ std::tuple<at::Tensor, at::Tensor> routed_experts_int4_cuda(const at::Tensor& h,
                                                             const at::Tensor& down_scale, int64_t intermediate,
                                                             int64_t group_size);
 
+// route_top_k_cuda (pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:37-40): (weights fp32
+// [tokens, k], experts int64 [tokens, k]) from logits [tokens, experts] whose rows may lie apart.
+std::tuple<at::Tensor, at::Tensor> route_top_k_cuda(const at::Tensor& logits, int64_t k);
+
+// silu_mul_cuda (ops.hpp:42-43): silu(x[:, :n]) * x[:, n:], silu rounded to the dtype.
+at::Tensor silu_mul_cuda(const at::Tensor& x);
+
 }  // namespace pulsarlm

@@ -295,3 +295,45 @@ def routed_experts_int4_cuda(h: torch.Tensor, top_experts: torch.Tensor, top_wei
               _DTYPES[gate_up[1].dtype], group_size, _ptr(offsets), _ptr(out), _ptr(ws),
               0 if ws is None else ws.numel(), _stream(h.device))
     return out, offsets
+
+
+def route_top_k_cuda(logits: torch.Tensor, k: int, experts_i32: bool = False):
+    """route_top_k_cuda (ops.hpp:37-40): (weights fp32 [T, k], experts int64 [T, k]) for
+    logits [T, E] whose rows may lie apart (unit column stride); experts_i32 gives int32
+    experts (what routed_experts_int4_cuda / plm_moe take) instead."""
+    op = "route_top_k"
+    _require(logits.is_cuda and logits.dim() == 2 and logits.stride(1) == 1, op,
+             "logits must be CUDA [tokens, experts], each row contiguous")
+    _require(logits.dtype in _DTYPES, op, "logits must be fp32, fp16 or bf16")
+    t, e = logits.shape
+    weights = torch.empty((t, k), dtype=torch.float32, device=logits.device)
+    chosen = torch.empty((t, k), dtype=torch.int32 if experts_i32 else torch.int64, device=logits.device)
+    stride = logits.stride(0) if t > 1 else e
+    with torch.cuda.device(logits.device):
+        _call("plm_route_top_k", _ptr(logits), _DTYPES[logits.dtype], t, e, stride, k, _ptr(weights),
+              None if experts_i32 else _ptr(chosen), _ptr(chosen) if experts_i32 else None, _stream(logits.device))
+    return weights, chosen
+
+
+def silu_mul_cuda(x: torch.Tensor) -> torch.Tensor:
+    """silu_mul_cuda (ops.hpp:42-43): silu(x[:, :n]) * x[:, n:], silu rounded to the dtype."""
+    op = "silu_mul"
+    _require(x.is_cuda and x.dim() == 2 and x.is_contiguous() and x.size(1) % 2 == 0, op,
+             "x must be contiguous CUDA [tokens, 2 * n]")
+    _require(x.dtype in _DTYPES, op, "x must be fp32, fp16 or bf16")
+    t, n = x.size(0), x.size(1) // 2
+    y = torch.empty((t, n), dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        _call("plm_silu_mul", _ptr(x), _DTYPES[x.dtype], t, n, _ptr(y), _stream(x.device))
+    return y
+
+
+def moe_block_int4_cuda(h: torch.Tensor, router_logits: torch.Tensor, top_k: int, gate_up: tuple, down: tuple,
+                        intermediate: int, group_size: int):
+    """The routed-experts half of a MoE block from the router's logits: route_top_k (int32
+    experts) then routed_experts with int4 experts and SiLU (qwen4_exp.cpp:542 followed by
+    paged_forward.cpp:108-130), all enqueued on the current stream with no host sync.
+    Returns (out [T, H], offsets int32 [E], top_weights fp32 [T, k], top_experts int32 [T, k])."""
+    weights, experts = route_top_k_cuda(router_logits, top_k, experts_i32=True)
+    out, offsets = routed_experts_int4_cuda(h, experts, weights, gate_up, down, intermediate, group_size)
+    return out, offsets, weights, experts

@@ -128,3 +128,32 @@ def test_linear_quantized_matches_dense(kind):
     assert y.shape == (3, 5, N)
     ref = _host.linear.dense(dense).apply(x)
     assert torch.allclose(y.float(), ref.float(), 2e-2, 2e-2)
+
+
+# ------------------------------------------------- router and activation (test_fused_ops.cpp)
+
+
+@pytest.mark.parametrize("dtype", [torch.float, torch.bfloat16])
+@pytest.mark.parametrize("experts", [16, 512])
+def test_route_top_k_picks_the_most_probable_experts(dtype, experts):
+    """test_fused_ops.cpp:83-100 through the C++ route_top_k_cuda."""
+    gen = torch.Generator(device="cuda").manual_seed(experts)
+    k = 10
+    logits = torch.randn(64, experts + 1, generator=gen, **cuda(dtype)).narrow(1, 0, experts)
+    weights, chosen = _host.route_top_k_cuda(logits, k)
+    probabilities = torch.softmax(logits, -1, dtype=torch.float)
+    top = torch.topk(probabilities, k, -1).values
+    assert chosen.dtype == torch.long
+    assert torch.allclose(probabilities.gather(1, chosen), top, 1e-6, 0.0)
+    assert torch.allclose(weights, top / top.sum(-1, True), 1e-6, 1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float, torch.bfloat16])
+def test_silu_mul_multiplies_silu_of_gate_by_up(dtype):
+    """test_fused_ops.cpp:102-111 through the C++ silu_mul_cuda."""
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(64, 2 * 256, generator=gen, **cuda(dtype))
+    got = _host.silu_mul_cuda(x)
+    expected = torch.nn.functional.silu(x.narrow(1, 0, 256)) * x.narrow(1, 256, 256)
+    tol = 1e-5 if dtype == torch.float else 1e-2
+    assert torch.allclose(got.float(), expected.float(), tol, tol)

@@ -305,3 +305,46 @@ def test_zipf_routing_is_skewed_and_distinct():
     counts = np.bincount(experts.reshape(-1), minlength=128)
     assert counts[0] > 5 * counts[64:].mean()
     assert np.allclose(w.sum(-1), 1.0, atol=1e-6)
+
+
+# ---------------------------------------------------------------- router and activation
+
+
+@pytest.mark.parametrize("experts,k", [(16, 10), (512, 10), (128, 8)])
+def test_route_top_k_ref_matches_torch(experts, k):
+    """The reference test's own checks (test_fused_ops.cpp:93-99) with torch on the CPU."""
+    logits = torch.randn(37, experts, generator=torch.Generator().manual_seed(experts))
+    w, e, _ = O.route_top_k_ref(logits.numpy(), k)
+    probabilities = torch.softmax(logits, -1, dtype=torch.float32)
+    top = torch.topk(probabilities, k, -1).values
+    got = probabilities.gather(1, torch.from_numpy(e))
+    assert torch.allclose(got, top, rtol=1e-6, atol=0.0)
+    assert torch.allclose(torch.from_numpy(w), top / top.sum(-1, keepdim=True), rtol=1e-6, atol=1e-6)
+    assert np.all(np.diff(np.take_along_axis(probabilities.numpy(), e, 1), axis=1) <= 0)  # descending
+
+
+def test_route_top_k_ref_breaks_ties_by_lower_expert():
+    logits = np.array([[1.0, 3.0, 3.0, 2.0, 3.0], [0.0, 0.0, 0.0, 0.0, 0.0]], dtype=np.float32)
+    w, e, _ = O.route_top_k_ref(logits, 5)
+    assert e.tolist() == [[1, 2, 4, 3, 0], [0, 1, 2, 3, 4]]
+    assert np.allclose(w[1], 0.2) and abs(w[0].sum() - 1) < 1e-6
+    _, e3, _ = O.route_top_k_ref(logits, 3)
+    assert e3.tolist() == [[1, 2, 4], [0, 1, 2]]
+    assert np.allclose(O.route_top_k_ref(logits, 3)[0][0], 1 / 3, atol=1e-7)  # three equal winners
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16", "fp16"])
+def test_silu_mul_ref_matches_torch(dtype):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((64, 2 * 96)) * 4).astype(np.float32)
+    x = x if dtype == "fp32" else O.round_to(x, dtype)
+    got = O.silu_mul_ref(x, dtype)
+    t = torch.from_numpy(x).double()
+    expected = (torch.nn.functional.silu(t[:, :96]) * t[:, 96:]).numpy()
+    tol = 1e-5 if dtype == "fp32" else 1e-2  # test_fused_ops.cpp:20-22
+    assert np.allclose(got, expected, rtol=tol, atol=tol)
+    # Closed forms: silu(0) = 0; silu(g) = g for large g, 0 for very negative g.
+    z = O.silu_mul_ref(np.array([[0.0, 60.0, -60.0, 1.0, 2.0, 3.0]], dtype=np.float32), dtype)
+    assert z[0, 0] == 0
+    assert z[0, 1] == 120.0  # silu(60) = 60 in fp32, times 2 (exact in every dtype)
+    assert abs(z[0, 2]) < 1e-20
