@@ -19,6 +19,17 @@ linear linear::fp8(const at::Tensor& weight, const at::Tensor& scale, std::int64
     return linear(quant_weight{std::move(w), std::move(s), weight.size(0), block_n, group_size, true});
 }
 
+linear linear::fp8_rows(const at::Tensor& weight, const at::Tensor& weight_scale_inv, std::int64_t block_n,
+                        std::int64_t block_k, const at::Tensor& row_order) {
+    TORCH_CHECK(row_order.dim() == 1 && row_order.size(0) == weight.size(0),
+                "linear: row_order must hold one index per weight row");
+    const at::Tensor order = row_order.to(weight.device(), at::kLong);
+    const at::Tensor row_scale =
+        weight_scale_inv.to(weight.device()).repeat_interleave(block_n, 0).narrow(0, 0, weight.size(0));
+    const at::Tensor rows = weight.view(at::kByte).index_select(0, order).view(at::kFloat8_e4m3fn);
+    return fp8(rows, row_scale.index_select(0, order).contiguous(), 1, block_k);
+}
+
 linear linear::int4(const at::Tensor& weight_packed, const at::Tensor& scale, std::int64_t block_n,
                     std::int64_t group_size) {
     auto [w, s] = repack_int4_marlin_cuda(weight_packed, scale, block_n, group_size);

@@ -23,6 +23,7 @@ PYBIND11_MODULE(_host, m) {
     py::class_<pulsarlm::linear>(m, "linear")
         .def_static("dense", &pulsarlm::linear::dense)
         .def_static("fp8", &pulsarlm::linear::fp8)
+        .def_static("fp8_rows", &pulsarlm::linear::fp8_rows)
         .def_static("int4", &pulsarlm::linear::int4)
         .def("apply", &pulsarlm::linear::apply);
 }

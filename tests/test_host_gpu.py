@@ -3,6 +3,7 @@
 generators (seeded here), same exactness and allclose(2e-2, 2e-2) checks. Plus the
 linear operator (linear.hpp) with the int4 alternative, on a 3-D input."""
 
+import numpy as np
 import pytest
 import torch
 
@@ -157,3 +158,43 @@ def test_silu_mul_multiplies_silu_of_gate_by_up(dtype):
     expected = torch.nn.functional.silu(x.narrow(1, 0, 256)) * x.narrow(1, 256, 256)
     tol = 1e-5 if dtype == torch.float else 1e-2
     assert torch.allclose(got.float(), expected.float(), tol, tol)
+
+
+# ------------------------------------------------- fp8 checkpoint ingest (weight_scale_inv)
+
+
+def _block_checkpoint(n, k, seed):
+    """A block-quantized fp8 checkpoint linear: the test_qwen3_5.cpp:301-311 quantizer on
+    bf16 N(0, 0.02) weights, 128 x 128 blocks (weight, weight_scale_inv fp32)."""
+    from oracle import oracle as O
+    rng = np.random.default_rng(seed)
+    w = O.round_to((rng.standard_normal((n, k)) * 0.02).astype(np.float32), "bf16")
+    codes, scale_inv = O.fp8_block_quantize(w, 128, 128)
+    weight = torch.from_numpy(codes).cuda().view(torch.float8_e4m3fn)
+    return weight, torch.from_numpy(scale_inv).cuda(), O.dequant_fp8(codes, scale_inv, 128, 128, "bf16")
+
+
+@pytest.mark.parametrize("n", [640, 5120 + 64])
+def test_fp8_checkpoint_linear(n):
+    """linear::fp8(weight, weight_scale_inv, 128, 128) as qwen3_5.cpp:52-63 builds it."""
+    k = 1024
+    weight, scale_inv, dense = _block_checkpoint(n, k, seed=n)
+    lin = _host.linear.fp8(weight, scale_inv, 128, 128)
+    x = torch.randn((2, 9, k), generator=gen(7), **cuda(torch.bfloat16))
+    ref = x.float() @ torch.from_numpy(dense).cuda().t()
+    assert torch.allclose(lin.apply(x).float(), ref, 2e-2, 2e-2)
+
+
+def test_fp8_checkpoint_permuted_rows():
+    """need_permuted_linear (qwen3_5.cpp:65-83): rows reordered across scale blocks
+    (an interleave within 128-row heads) after expanding the scales to one per row."""
+    n, k, head = 512, 768, 128
+    weight, scale_inv, dense = _block_checkpoint(n, k, seed=3)
+    within = torch.cat([torch.arange(0, head, 2), torch.arange(1, head, 2)])
+    order = torch.cat([h * head + within for h in range(n // head)])
+    order = order.view(-1, head).flip(0).reshape(-1)  # heads reversed too: rows cross blocks
+    lin = _host.linear.fp8_rows(weight, scale_inv, 128, 128, order)
+    for m in (1, 16, 200):
+        x = torch.randn((m, k), generator=gen(m), **cuda(torch.bfloat16))
+        ref = x.float() @ torch.from_numpy(dense).cuda()[order.cuda()].t()
+        assert torch.allclose(lin.apply(x).float(), ref, 2e-2, 2e-2), m
