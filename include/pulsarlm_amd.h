@@ -204,6 +204,20 @@ int plm_route_top_k(const void* logits, plm_dtype dtype, int64_t tokens, int64_t
  */
 int plm_silu_mul(const void* x, plm_dtype dtype, int64_t tokens, int64_t n, void* y, void* stream);
 
+/*
+ * Non-repacked int4 GEMM: y [M, N] = x [M, K] @ W^T in x_dtype (PLM_BF16 or PLM_FP16),
+ * W[n, k] = round(fp32(q[n, k] * scale[n, k / group_size])) with q the signed nibbles of
+ * weight_packed int32 [N, K/8] (least significant first) and weight_scale fp32 [N, K/g],
+ * read in place (no repack). num_splits = 0 picks the K split; >= 1 forces it (the extra
+ * splits past the K tiles contribute zero). The split partials go to the workspace
+ * (plm_gemm_int4_plain_workspace_bytes; no zeroing needed) and are summed in split order.
+ * Replaces gemm_int4_cuda / gemm_int4_split_cuda (ops.hpp:269-297, int4_gemm.cu:153-478).
+ */
+int64_t plm_gemm_int4_plain_workspace_bytes(int64_t m, int64_t n, int64_t k, int64_t num_splits);
+int plm_gemm_int4_plain(const void* x, plm_dtype x_dtype, const int32_t* weight_packed, const float* weight_scale,
+                        int64_t m, int64_t n, int64_t k, int64_t group_size, int64_t num_splits, void* y,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,6 +36,8 @@ SIGNATURES = {
                                 _P]),
     "plm_grouped_gemm_workspace_bytes": (_I64, [_I64, _I64]),
     "plm_moe_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "plm_gemm_int4_plain_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "plm_gemm_int4_plain": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ, _P]),
     "plm_route_top_k": (_INT, [_P, _INT, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
     "plm_silu_mul": (_INT, [_P, _INT, _I64, _I64, _P, _P]),
     "plm_moe": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _INT, _I64, _P, _P, _P, _SZ,

@@ -20,7 +20,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libpulsarlm_amd.so"
 
-SOURCES = ["repack.hip", "gemm_decode.hip", "gemm_mfma.hip", "quant.hip", "moe.hip", "routing.hip", "capi.hip"]
+SOURCES = ["repack.hip", "gemm_decode.hip", "gemm_mfma.hip", "quant.hip", "moe.hip", "routing.hip", "gemm_plain.hip", "capi.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

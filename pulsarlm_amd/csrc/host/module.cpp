@@ -20,6 +20,8 @@ PYBIND11_MODULE(_host, m) {
     m.def("routed_experts_int4_cuda", &pulsarlm::routed_experts_int4_cuda);
     m.def("route_top_k_cuda", &pulsarlm::route_top_k_cuda);
     m.def("silu_mul_cuda", &pulsarlm::silu_mul_cuda);
+    m.def("gemm_int4_cuda", &pulsarlm::gemm_int4_cuda);
+    m.def("gemm_int4_split_cuda", &pulsarlm::gemm_int4_split_cuda);
     py::class_<pulsarlm::linear>(m, "linear")
         .def_static("dense", &pulsarlm::linear::dense)
         .def_static("fp8", &pulsarlm::linear::fp8)

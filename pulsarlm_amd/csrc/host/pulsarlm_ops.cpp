@@ -288,4 +288,40 @@ at::Tensor silu_mul_cuda(const at::Tensor& x) {
     return y;
 }
 
+namespace {
+at::Tensor gemm_int4_plain(const char* op, const at::Tensor& x, const at::Tensor& weight_packed,
+                           const at::Tensor& weight_scale, int64_t group_size, int64_t num_splits) {
+    TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.is_contiguous(), op, ": x must be a contiguous CUDA [M, K] tensor");
+    TORCH_CHECK(weight_packed.is_cuda() && weight_packed.scalar_type() == at::kInt && weight_packed.dim() == 2 &&
+                    weight_packed.is_contiguous(),
+                op, ": weight_packed must be contiguous CUDA int32 [N, K/8]");
+    const int64_t m = x.size(0), k = x.size(1), n = weight_packed.size(0);
+    TORCH_CHECK(weight_packed.size(1) * 8 == k, op, ": weight_packed must be [N, K/8]");
+    TORCH_CHECK(group_size > 0 && weight_scale.dim() == 2 && weight_scale.size(0) == n &&
+                    weight_scale.size(1) * group_size == k,
+                op, ": weight_scale must be [N, K/group_size]");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    const at::Tensor scale = weight_scale.to(at::kFloat).contiguous();
+    at::Tensor y = at::empty({m, n}, x.options());
+    const int64_t nbytes = plm_gemm_int4_plain_workspace_bytes(m, n, k, num_splits);
+    at::Tensor ws = nbytes > 0 ? at::empty({nbytes}, x.options().dtype(at::kByte)) : at::Tensor();
+    check_rc(plm_gemm_int4_plain(x.data_ptr(), dtype_of(op, x.scalar_type()),
+                                 static_cast<const int32_t*>(weight_packed.data_ptr()),
+                                 static_cast<const float*>(scale.data_ptr()), m, n, k, group_size, num_splits,
+                                 y.data_ptr(), ptr(ws), ws.defined() ? ws.numel() : 0, stream_of(x)));
+    return y;
+}
+}  // namespace
+
+at::Tensor gemm_int4_cuda(const at::Tensor& x, const at::Tensor& weight_packed, const at::Tensor& weight_scale,
+                          int64_t group_size) {
+    return gemm_int4_plain("gemm_int4", x, weight_packed, weight_scale, group_size, 0);
+}
+
+at::Tensor gemm_int4_split_cuda(const at::Tensor& x, const at::Tensor& weight_packed,
+                                const at::Tensor& weight_scale, int64_t group_size, int64_t num_splits) {
+    TORCH_CHECK(num_splits >= 1, "gemm_int4: num_splits must be >= 1");
+    return gemm_int4_plain("gemm_int4", x, weight_packed, weight_scale, group_size, num_splits);
+}
+
 }  // namespace pulsarlm

@@ -80,4 +80,12 @@ std::tuple<at::Tensor, at::Tensor> route_top_k_cuda(const at::Tensor& logits, in
 // silu_mul_cuda (ops.hpp:42-43): silu(x[:, :n]) * x[:, n:], silu rounded to the dtype.
 at::Tensor silu_mul_cuda(const at::Tensor& x);
 
+// gemm_int4_cuda / gemm_int4_split_cuda (pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:269-297):
+// y [M, N] = x @ W^T with W = round(fp32(q * scale)) from weight_packed int32 [N, K/8] and
+// weight_scale fp32 [N, K/group_size], read in place; the split variant forces num_splits.
+at::Tensor gemm_int4_cuda(const at::Tensor& x, const at::Tensor& weight_packed, const at::Tensor& weight_scale,
+                          int64_t group_size);
+at::Tensor gemm_int4_split_cuda(const at::Tensor& x, const at::Tensor& weight_packed,
+                                const at::Tensor& weight_scale, int64_t group_size, int64_t num_splits);
+
 }  // namespace pulsarlm

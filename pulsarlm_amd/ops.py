@@ -337,3 +337,37 @@ def moe_block_int4_cuda(h: torch.Tensor, router_logits: torch.Tensor, top_k: int
     weights, experts = route_top_k_cuda(router_logits, top_k, experts_i32=True)
     out, offsets = routed_experts_int4_cuda(h, experts, weights, gate_up, down, intermediate, group_size)
     return out, offsets, weights, experts
+
+
+def _gemm_int4_plain(op: str, x: torch.Tensor, weight_packed: torch.Tensor, weight_scale: torch.Tensor,
+                     group_size: int, num_splits: int) -> torch.Tensor:
+    _require(x.is_cuda and x.dim() == 2 and x.dtype in (torch.float16, torch.bfloat16), op,
+             "x must be a CUDA [M, K] fp16/bf16 tensor")
+    _require(weight_packed.dtype == torch.int32 and weight_packed.dim() == 2, op, "weight_packed must be int32 [N, K/8]")
+    m, k = x.shape
+    n = weight_packed.shape[0]
+    _require(weight_packed.shape[1] * 8 == k, op, "weight_packed must be [N, K/8]")
+    _require(weight_scale.dim() == 2 and tuple(weight_scale.shape) == (n, k // group_size) if group_size > 0 else False,
+             op, "weight_scale must be [N, K/group_size]")
+    scale = weight_scale.to(torch.float32).contiguous()
+    y = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    lib = _lib.load()
+    nbytes = lib.plm_gemm_int4_plain_workspace_bytes(m, n, k, num_splits)
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=x.device) if nbytes > 0 else None
+    with torch.cuda.device(x.device):
+        _call("plm_gemm_int4_plain", _ptr(x.contiguous()), _DTYPES[x.dtype], _ptr(weight_packed.contiguous()),
+              _ptr(scale), m, n, k, group_size, num_splits, _ptr(y), _ptr(ws), 0 if ws is None else ws.numel(),
+              _stream(x.device))
+    return y
+
+
+def gemm_int4_cuda(x: torch.Tensor, weight_packed: torch.Tensor, weight_scale: torch.Tensor, group_size: int):
+    """gemm_int4_cuda (ops.hpp:269-285): the non-repacked int4 GEMM, W = round(fp32(q * scale))."""
+    return _gemm_int4_plain("gemm_int4", x, weight_packed, weight_scale, group_size, 0)
+
+
+def gemm_int4_split_cuda(x: torch.Tensor, weight_packed: torch.Tensor, weight_scale: torch.Tensor, group_size: int,
+                         num_splits: int):
+    """gemm_int4_split_cuda (ops.hpp:287-297): the same with the K split forced to num_splits (>= 1)."""
+    _require(num_splits >= 1, "gemm_int4", "num_splits must be >= 1")
+    return _gemm_int4_plain("gemm_int4", x, weight_packed, weight_scale, group_size, num_splits)

@@ -348,3 +348,17 @@ def test_silu_mul_ref_matches_torch(dtype):
     assert z[0, 0] == 0
     assert z[0, 1] == 120.0  # silu(60) = 60 in fp32, times 2 (exact in every dtype)
     assert abs(z[0, 2]) < 1e-20
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_dequant_plain_int4_every_nibble(dtype):
+    """Every nibble x a sweep of fp32 scales against torch: the product rounded to fp32,
+    then to the dtype (int4_gemm.cu:136-138: pack2(q * scale))."""
+    rng = np.random.default_rng(9)
+    q = np.tile(np.arange(-8, 8), 64)[None, :].repeat(40, 0)  # [40, 1024]
+    scale = (rng.random((40, 1024 // 16)) * 0.2 + 1e-4).astype(np.float32)
+    got = O.dequant_int4_plain(O.pack_int4(q), scale, 16, dtype)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    exp = torch.from_numpy(scale).repeat_interleave(16, 1)
+    ref = (torch.from_numpy(q).float() * exp).to(tdt).float().numpy()
+    assert np.array_equal(got, ref)
