@@ -154,26 +154,28 @@ __global__ void __launch_bounds__(1024) moe_tiles_kernel(const int32_t* __restri
     }
 }
 
-// Two-level tile lists for skewed groups: expert e's rows in full blocks of 256 (a last
-// block of at least 192 rows counts as full) go to `big`, the remaining rows (< 192) to
-// `small` in blocks of 64. Slots past the last tile of either list get rows = 0.
-__device__ __forceinline__ void tiles2_split(int32_t c, int32_t& nbig, int32_t& rem) {
-    nbig = c / 256;
-    rem = c - nbig * 256;
-    if (rem >= 192) ++nbig, rem = 0;
+// Two-level tile lists for skewed groups: expert e's rows in full blocks of `bb` rows (a
+// last block of at least `full` rows counts as full) go to `big`, the remaining rows
+// (< full) to `small` in blocks of `sb`, so a heavily routed expert's weights are read once
+// per big block instead of once per small one. Slots past the last tile get rows = 0.
+__device__ __forceinline__ void tiles2_split(int32_t c, int bb, int full, int32_t& nbig, int32_t& rem) {
+    nbig = c / bb;
+    rem = c - nbig * bb;
+    if (rem >= full) ++nbig, rem = 0;
 }
 
 __global__ void __launch_bounds__(1024) moe_tiles2_kernel(const int32_t* __restrict__ offsets, int n_experts,
-                                                           int64_t max_big, int64_t max_small,
-                                                           int32_t* __restrict__ big, int32_t* __restrict__ small) {
+                                                           int bb, int sb, int full, int64_t max_big,
+                                                           int64_t max_small, int32_t* __restrict__ big,
+                                                           int32_t* __restrict__ small) {
     __shared__ int32_t buf[1024];
     __shared__ int32_t first_big[4096];
     __shared__ int32_t first_small[4096];
     for (int e = threadIdx.x; e < n_experts; e += 1024) {
         int32_t nbig, rem;
-        tiles2_split(offsets[e] - (e == 0 ? 0 : offsets[e - 1]), nbig, rem);
+        tiles2_split(offsets[e] - (e == 0 ? 0 : offsets[e - 1]), bb, full, nbig, rem);
         first_big[e] = nbig;
-        first_small[e] = (rem + 63) / 64;
+        first_small[e] = (rem + sb - 1) / sb;
     }
     __syncthreads();
     const int32_t n_big = block_exclusive_scan(first_big, n_experts, buf);
@@ -181,18 +183,18 @@ __global__ void __launch_bounds__(1024) moe_tiles2_kernel(const int32_t* __restr
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
         const int32_t lo = e == 0 ? 0 : offsets[e - 1], hi = offsets[e];
         int32_t nbig, rem;
-        tiles2_split(hi - lo, nbig, rem);
+        tiles2_split(hi - lo, bb, full, nbig, rem);
         int32_t r = lo, t = first_big[e];
-        for (int b = 0; b < nbig; ++b, ++t, r += 256) {
+        for (int b = 0; b < nbig; ++b, ++t, r += bb) {
             big[3 * t] = e;
             big[3 * t + 1] = r;
-            big[3 * t + 2] = min(256, hi - r);
+            big[3 * t + 2] = min(bb, hi - r);
         }
         t = first_small[e];
-        for (; r < hi; r += 64, ++t) {
+        for (; r < hi; r += sb, ++t) {
             small[3 * t] = e;
             small[3 * t + 1] = r;
-            small[3 * t + 2] = min(64, hi - r);
+            small[3 * t + 2] = min(sb, hi - r);
         }
     }
     for (int64_t t = n_big + threadIdx.x; t < max_big; t += blockDim.x) big[3 * t + 2] = 0;
@@ -284,9 +286,13 @@ moe_ws moe_layout(int64_t tokens, int64_t top_k, int64_t n_experts, int64_t hidd
 // How a grouped GEMM over `rows` sorted rows is tiled. With many rows per expert (skewed
 // routing at large batch), full 256-row blocks run on the 256 x 256 shape and the rest on
 // 64-row tiles (two launches); otherwise one shape sized to the average rows per expert.
+// (At T = 256 of the Zipf-routed benchmark block, 64-row blocks for the heavy experts and
+// 16-row tiles for the rest measured slower than 16-row tiles throughout: the repeated
+// weight reads of a heavy expert's concurrent tiles hit in L2.)
 struct grouped_plan {
     bool two;
-    int shape;
+    int shape, shape_b;   // shapes of the first and second list
+    int bb, sb, full;     // two lists: big and small block rows, rows that count as a full big block
     int64_t max_a, max_b;  // tile slots of the first and second list
     int64_t slots() const { return max_a + max_b; }
 };
@@ -295,9 +301,14 @@ grouped_plan plan_grouped(int64_t rows, int64_t n_experts) {
     grouped_plan p{};
     p.two = rows >= 128 * n_experts;
     if (p.two) {
-        p.shape = 4;
-        p.max_a = rows / 192 + 1;
-        p.max_b = std::min<int64_t>(3 * n_experts, ceil_div(rows, 64));
+        p.shape = 4, p.shape_b = 1;  // 256 x 256 blocks, then 64-row tiles
+        p.bb = 256, p.sb = 64, p.full = 192;
+    }
+    if (p.two) {
+        p.max_a = rows / p.full + 1;
+        // Each expert leaves fewer than `full` rows, in at most ceil(full / sb) small tiles, and
+        // the small tiles hold all remaining rows plus at most one partial tile per expert.
+        p.max_b = std::min<int64_t>(ceil_div(p.full, p.sb) * n_experts, ceil_div(rows, p.sb) + n_experts);
     } else {
         p.shape = grouped_shape_for(rows, n_experts);
         p.max_a = ceil_div(rows, grouped_block_rows(p.shape)) + n_experts;
@@ -329,7 +340,8 @@ int launch_sort(const char* op, const int32_t* experts, const float* weights, in
 int launch_tiles(const char* op, const int32_t* offsets, int64_t n_experts, const grouped_plan& p, int32_t* tiles,
                  hipStream_t s) {
     if (p.two)
-        moe_tiles2_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), p.max_a, p.max_b, tiles, tiles + 3 * p.max_a);
+        moe_tiles2_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), p.bb, p.sb, p.full, p.max_a, p.max_b, tiles,
+                                             tiles + 3 * p.max_a);
     else
         moe_tiles_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), grouped_block_rows(p.shape), p.max_a, tiles);
     PLM_HIP_LAUNCH_CHECK(op);
@@ -344,7 +356,7 @@ int launch_plan(const char* op, const grouped_plan& p, const void* x, bool bf16,
         return rc;
     if (!p.two) return PLM_OK;
     return launch_grouped(op, PLM_INT4, x, bf16, w, scale, scale_dtype, rows, n, k, block_n, group_size, y,
-                          tiles + 3 * p.max_a, p.max_b, row_index, 1, s);
+                          tiles + 3 * p.max_a, p.max_b, row_index, p.shape_b, s);
 }
 
 }  // namespace

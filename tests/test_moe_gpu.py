@@ -35,11 +35,14 @@ def _experts(e, n, k, g, seed):
     return w, s, deq
 
 
-# The last two cases have >= 128 rows per expert on average, which tiles full 256-row blocks
-# (including a last block of >= 192 rows) on the 256 x 256 shape and the rest on 64-row tiles.
+# Below 128 rows per expert on average one shape sized to the average runs; from 128, full
+# 256-row blocks (a last block of >= 192 rows counts as full) run on the 256 x 256 shape and
+# the rest on 64-row tiles. [129] * 8 gives every expert the most 64-row tiles its remainder
+# allows (3 each), more than the remaining rows alone would need.
 @pytest.mark.parametrize("counts", [[5, 0, 17, 1, 0, 40, 3, 34], [0, 0, 0, 100, 0, 0, 0, 0], [1] * 8,
                                     [300, 20, 0, 2, 9, 0, 120, 61], [700, 130, 0, 200, 0, 0, 0, 0],
-                                    [256, 512, 191, 192, 64, 63, 1, 0]])
+                                    [256, 512, 191, 192, 64, 63, 1, 0], [33] * 8, [129] * 8,
+                                    [17, 33, 49, 1, 63, 65, 0, 47]])
 def test_grouped_gemm_matches_per_expert_reference(counts):
     e, n, k, g = 8, 520, 1024, 128
     w, s, deq = _experts(e, n, k, g, seed=sum(counts))
