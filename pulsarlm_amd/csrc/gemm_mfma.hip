@@ -50,6 +50,7 @@ struct mfma_args {
     int ktiles, strips, groups, group_size;
     int splits, tiles_per_split;
     int m_blocks, n_blocks;
+    int tile_base;  // plain calls: this launch's work tiles start at tile_base
     // A8
     const uint8_t* xq;      // e4m3 [M][ktiles][128], lane-permuted within each tile
     const float* x_scale;   // [M]
@@ -111,8 +112,9 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         rows = a.tiles[3 * tile + 2];
         if (rows <= 0) return;  // uniform across the workgroup
     } else {
-        const int mb = blockIdx.x % a.m_blocks;
-        nb = blockIdx.x / a.m_blocks;
+        const int tile = blockIdx.x + a.tile_base;
+        const int mb = tile % a.m_blocks;
+        nb = tile / a.m_blocks;
         row0 = mb * BM;
         rows = min(BM, a.m - row0);
     }
@@ -372,7 +374,16 @@ struct mfma_config {
     int shape;  // 0 small, 1 large, 2 huge, 3 rows64, 4 rows16, 5 wide, 6 tall
     int m_blocks, n_blocks;
     int splits, tiles_per_split;
+    // Two launches when the tiles fill the CUs a whole number of times plus at most half a
+    // round: the last tail_tiles work tiles run second, with K split tail_splits ways, so
+    // the last round is shorter instead of half empty.
+    int tail_tiles, tail_splits, tail_tiles_per_split;
 };
+
+bool no_tail() {
+    static const bool off = getenv("PLM_MFMA_NO_TAIL") != nullptr;  // A/B measurements
+    return off;
+}
 
 // Tile shape and split count: the candidate with the least estimated time, counting whole
 // rounds of workgroups over the CUs, a fixed cost of about three K tiles per workgroup
@@ -392,14 +403,29 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
             splits = std::max<int64_t>(1, std::min<int64_t>(ceil_div(cus, tiles), ktiles / 4));
         c.tiles_per_split = static_cast<int>(ceil_div(ktiles, splits));
         c.splits = static_cast<int>(ceil_div(ktiles, c.tiles_per_split));
+        const int64_t rem = tiles % cus;
+        if (c.splits == 1 && tiles > cus && rem > 0 && 2 * rem <= cus && rem <= kMaxCounters && ktiles >= 8 &&
+            !no_tail()) {
+            const int64_t ts = std::min<int64_t>(cus / rem, ktiles / 4);
+            c.tail_tiles_per_split = static_cast<int>(ceil_div(ktiles, ts));
+            c.tail_splits = static_cast<int>(ceil_div(ktiles, c.tail_tiles_per_split));
+            if (c.tail_splits >= 2) c.tail_tiles = static_cast<int>(rem);
+        }
         return c;
     };
     auto cost = [&](const mfma_config& c) {
         const shape sh = shape_of(c.shape);
-        const int64_t rounds = ceil_div(static_cast<int64_t>(c.m_blocks) * c.n_blocks * c.splits, cus);
+        const double area = static_cast<double>(sh.bm()) * sh.bs() / kShapeRate[c.shape];
+        const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
+        if (c.tail_tiles > 0) {
+            const int64_t full_rounds = (tiles - c.tail_tiles) / cus;
+            return (static_cast<double>(full_rounds) * (c.tiles_per_split + 3) + c.tail_tiles_per_split + 3 +
+                    0.5 * c.tail_splits) * area;
+        }
+        const int64_t rounds = ceil_div(tiles * c.splits, cus);
         // The last workgroup of a split tile reads every split's partials: half a K tile each.
         const double reduce = c.splits > 1 ? 0.5 * c.splits : 0.0;
-        return static_cast<double>(rounds) * (c.tiles_per_split + 3 + reduce) * sh.bm() * sh.bs() / kShapeRate[c.shape];
+        return static_cast<double>(rounds) * (c.tiles_per_split + 3 + reduce) * area;
     };
     if (const char* env = getenv("PLM_MFMA")) {  // tuning sweeps: S, L, H or R
         const int id = env[0] == 'X' ? 6 : env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
@@ -416,9 +442,10 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
 
 int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k) {
     const mfma_config c = choose_mfma(f, m, n, k);
-    if (c.splits <= 1) return 0;
     const shape sh = shape_of(c.shape);
     const int64_t tile_bytes = static_cast<int64_t>(sh.bm()) * sh.bs() * kTileN * 4;
+    if (c.tail_tiles > 0) return kCounterBytes + static_cast<int64_t>(c.tail_tiles) * c.tail_splits * tile_bytes;
+    if (c.splits <= 1) return 0;
     return kCounterBytes + static_cast<int64_t>(c.m_blocks) * c.n_blocks * c.splits * tile_bytes;
 }
 
@@ -518,7 +545,7 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
     a.n_blocks = c.n_blocks;
     a.xq = xq;
     a.x_scale = x_scale;
-    if (c.splits > 1) {
+    if (c.splits > 1 || c.tail_tiles > 0) {
         const int64_t need = mfma_workspace_bytes(f, m, n, k);
         if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need) {
             set_error(op, "workspace of %lld bytes required, %zu given", static_cast<long long>(need), workspace_bytes);
@@ -527,8 +554,20 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
         a.counters = static_cast<uint32_t*>(workspace);
         a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     }
-    dim3 grid(c.m_blocks * c.n_blocks, c.splits);
-    launch_all<false>(f, bf16, a, c.shape, group_size % kTileK == 0, xq != nullptr, grid, s);
+    const bool uniform = group_size % kTileK == 0;
+    const int tiles = c.m_blocks * c.n_blocks;
+    if (c.tail_tiles > 0) {
+        // Whole rounds of unsplit tiles, then the tail tiles with K split.
+        launch_all<false>(f, bf16, a, c.shape, uniform, xq != nullptr, dim3(tiles - c.tail_tiles, 1), s);
+        PLM_HIP_LAUNCH_CHECK(op);
+        a.tile_base = tiles - c.tail_tiles;
+        a.splits = c.tail_splits;
+        a.tiles_per_split = c.tail_tiles_per_split;
+        launch_all<false>(f, bf16, a, c.shape, uniform, xq != nullptr, dim3(c.tail_tiles, c.tail_splits), s);
+        PLM_HIP_LAUNCH_CHECK(op);
+        return PLM_OK;
+    }
+    launch_all<false>(f, bf16, a, c.shape, uniform, xq != nullptr, dim3(tiles, c.splits), s);
     PLM_HIP_LAUNCH_CHECK(op);
     return PLM_OK;
 }
