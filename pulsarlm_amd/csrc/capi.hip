@@ -17,7 +17,7 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
 int launch_quantize_rows(const char* op, const void* x, bool bf16, int64_t m, int64_t k, uint8_t* out, float* sx,
                          bool permuted, hipStream_t s);
 int64_t decode_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k);
-int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k);
+int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k, bool a8);
 
 constexpr int64_t kDecodeMaxM = 16;
 
@@ -53,7 +53,7 @@ extern "C" {
 
 int64_t plm_gemm_workspace_bytes(plm_format format, int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0) return 0;
-    return m <= kDecodeMaxM ? decode_workspace_bytes(format, m, n, k) : mfma_workspace_bytes(format, m, n, k);
+    return m <= kDecodeMaxM ? decode_workspace_bytes(format, m, n, k) : mfma_workspace_bytes(format, m, n, k, false);
 }
 
 int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype, const void* weight, const void* scale,
@@ -84,7 +84,7 @@ w8a8_ws w8a8_layout(int64_t m, int64_t n, int64_t k) {
     w8a8_ws w{};
     // The split-K counters always keep the front of the workspace, even when this call
     // does not split, so scratch written here never lands on them.
-    const int64_t gemm = m <= kDecodeMaxM ? decode_workspace_bytes(PLM_FP8, m, n, k) : mfma_workspace_bytes(PLM_FP8, m, n, k);
+    const int64_t gemm = m <= kDecodeMaxM ? decode_workspace_bytes(PLM_FP8, m, n, k) : mfma_workspace_bytes(PLM_FP8, m, n, k, true);
     w.gemm = round_up(std::max<int64_t>(gemm, kCounterBytes), 256);
     w.xq = round_up(m * ceil_div(k, kTileK) * kTileK, 256);
     w.sx = round_up(m * 4, 256);

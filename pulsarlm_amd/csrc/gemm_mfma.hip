@@ -388,7 +388,10 @@ bool no_tail() {
 // Tile shape and split count: the candidate with the least estimated time, counting whole
 // rounds of workgroups over the CUs, a fixed cost of about three K tiles per workgroup
 // (pipeline fill, epilogue) and half a K tile per split for the split-K reduction.
-mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
+// The 256-row shapes with 12 or 16 strips need int4 weights, or fp8 weights with e4m3 x
+// (W8A8): with bf16 x and 2 KiB fp8 tiles two stages would not fit the 160 KiB LDS.
+mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) {
+    const bool wide_ok = f == PLM_INT4 || a8;
     const int64_t cus = cu_count();
     const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
     auto config = [&](int id) {
@@ -415,7 +418,10 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
     };
     auto cost = [&](const mfma_config& c) {
         const shape sh = shape_of(c.shape);
-        const double area = static_cast<double>(sh.bm()) * sh.bs() / kShapeRate[c.shape];
+        // fp8 W8A16 (2 KiB weight tiles dequantized to bf16): 128 x 128 measured 10-15 %
+        // slower than 256 x 128 at the Qwen3-27B shapes, unlike int4.
+        const double rate = f == PLM_FP8 && !a8 && c.shape == 0 ? 0.5 : kShapeRate[c.shape];
+        const double area = static_cast<double>(sh.bm()) * sh.bs() / rate;
         const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
         if (c.tail_tiles > 0) {
             const int64_t full_rounds = (tiles - c.tail_tiles) / cus;
@@ -429,19 +435,19 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k) {
     };
     if (const char* env = getenv("PLM_MFMA")) {  // tuning sweeps: S, L, H or R
         const int id = env[0] == 'X' ? 6 : env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
-        return config((id == 2 || id >= 5) && f != PLM_INT4 ? 1 : id);
+        return config((id == 2 || id >= 5) && !wide_ok ? 1 : id);
     }
     mfma_config best = config(0);
     for (int id : {1, 2, 3, 5, 6}) {
-        if ((id == 2 || id >= 5) && f != PLM_INT4) continue;
+        if ((id == 2 || id >= 5) && !wide_ok) continue;
         const mfma_config c = config(id);
         if (cost(c) < cost(best)) best = c;
     }
     return best;
 }
 
-int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k) {
-    const mfma_config c = choose_mfma(f, m, n, k);
+int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) {
+    const mfma_config c = choose_mfma(f, m, n, k, a8);
     const shape sh = shape_of(c.shape);
     const int64_t tile_bytes = static_cast<int64_t>(sh.bm()) * sh.bs() * kTileN * 4;
     if (c.tail_tiles > 0) return kCounterBytes + static_cast<int64_t>(c.tail_tiles) * c.tail_splits * tile_bytes;
@@ -452,7 +458,7 @@ int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k) {
 namespace {
 template <plm_format F, bool BF16, bool UNIFORM, bool WIDE, bool A8, bool GROUPED>
 void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
-    if constexpr (F == PLM_INT4 && !A8 && !GROUPED) {
+    if constexpr (((F == PLM_INT4 && !A8) || (F == PLM_FP8 && A8)) && !GROUPED) {
         if (shape == 2) {
             mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kHuge.wm, kHuge.wn, kHuge.mt, kHuge.ns>
                 <<<grid, kHuge.wm * kHuge.wn * 64, 0, s>>>(a);
@@ -536,7 +542,8 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
                 plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y,
                 void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq, const float* x_scale) {
     PLM_CHECK_ARG(k <= (int64_t{1} << 21), op, "K above 2^21 is not supported");
-    const mfma_config c = choose_mfma(f, m, n, k);
+    const bool a8 = xq != nullptr;
+    const mfma_config c = choose_mfma(f, m, n, k, a8);
     mfma_args a{};
     fill_common(a, x, w, scale, scale_dtype, m, n, k, block_n, group_size, y);
     a.splits = c.splits;
@@ -546,7 +553,7 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
     a.xq = xq;
     a.x_scale = x_scale;
     if (c.splits > 1 || c.tail_tiles > 0) {
-        const int64_t need = mfma_workspace_bytes(f, m, n, k);
+        const int64_t need = mfma_workspace_bytes(f, m, n, k, a8);
         if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need) {
             set_error(op, "workspace of %lld bytes required, %zu given", static_cast<long long>(need), workspace_bytes);
             return PLM_ERR_WORKSPACE;
