@@ -287,3 +287,15 @@ def test_decode_and_mfma_kernels_agree():
     a = ops.gemm_int4_marlin_cuda(x[:16].contiguous(), w, sc, n, 1, 128)
     b = ops.gemm_int4_marlin_cuda(x, w, sc, n, 1, 128)[:16]
     assert torch.allclose(a.float(), b.float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("m", [1, 4, 7, 16])
+@pytest.mark.parametrize("n,k,g", [(16, 128, 128), (48, 128, 128), (40, 256, 256), (1000, 384, 128)])
+def test_decode_small_k_and_narrow_n(m, n, k, g):
+    """Decode kernels where most wavefronts of a workgroup own no K tile (K of 1-3 tiles),
+    a single strip (N = 16) and a 256-wide scale group spanning two tiles."""
+    packed, s = int4_case(n, k, g, 1, seed=n + k + m)
+    w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), scale_tensor(s), 1, g)
+    x = x_case(m, k, "bf16", seed=m)
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, torch.bfloat16), w, sc, n, 1, g)
+    assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, g), None), f"m={m} n={n} k={k}")
