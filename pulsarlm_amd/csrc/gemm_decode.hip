@@ -327,6 +327,9 @@ struct rr_args {
     int x_bytes;      // per-wavefront x area: M rows x slots x 256 B, rounded to 1 KiB
     int wave_bytes;   // per-wavefront LDS area (x, then scales)
     int scale_dtype;
+    // W8A8: e4m3 x in the quantizer's lane-permuted layout [M][ktiles][128] and row scales.
+    const uint8_t* xq;
+    const float* x_scale;
 };
 
 template <int SC> struct rr_scale {
@@ -335,8 +338,13 @@ template <int SC> struct rr_scale {
     static constexpr int parts_shift = SC == 0 ? 1 : (SC == 1 ? 2 : 0);
 };
 
-template <plm_format F, bool BF16, int SG, int NW, int CH, int SC>
+//
+// A8 (W8A8, fp8 weights): x is the per-token e4m3 copy, staged 128 bytes per (row, tile);
+// each tile and strip is one v_mfma_scale_f32_16x16x128_f8f6f4 on the raw weight bytes, its
+// partial scaled by the weight block scale, and the row scales applied at the end.
+template <plm_format F, bool BF16, int SG, int NW, int CH, int SC, bool A8 = false>
 __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
+    static_assert(!A8 || F == PLM_FP8, "W8A8 takes fp8 weights");
     constexpr int TB = fmt_traits<F>::tile_bytes;
     constexpr int NL = TB / 1024;  // 16-byte loads per lane per tile
     constexpr int EB = rr_scale<SC>::eb, CS = rr_scale<SC>::cs, PS = rr_scale<SC>::parts_shift;
@@ -354,8 +362,17 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
     uint8_t* xs = rr_lds + wave * a.wave_bytes;
     uint8_t* ss = xs + a.x_bytes;
 
-    // x: 16-byte chunk j = (row, slot i, column o), LDS [row][slot][256 B].
-    {
+    // x: 16-byte chunk j = (row, slot i, column o), LDS [row][slot][256 B] (A8: 128 B of e4m3).
+    if constexpr (A8) {
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xq, static_cast<uint32_t>(a.m) * a.ktiles * kTileK);
+        const int total = a.m << (a.nkt_shift + 3);
+        for (int c = 0; c * 64 < total; ++c) {  // wave-uniform
+            const int j = c * 64 + lane;
+            const int o = j & 7, i = (j >> 3) & (slots - 1), row = j >> (a.nkt_shift + 3);
+            const int off = (row < a.m && i < nkt_w) ? (row * a.ktiles + wave + NW * i) * kTileK + (o << 4) : kOOB;
+            buffer_load_lds16(xr, xs + c * 1024, off, 0);
+        }
+    } else {
         const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, static_cast<uint32_t>(a.m) * a.k * 2);
         const int total = a.m << (a.nkt_shift + 4);
         for (int c = 0; c * 64 < total; ++c) {  // wave-uniform
@@ -418,6 +435,23 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
         for (int ii = 0; ii < CH; ++ii) {
             const int i = i0 + ii;
             if (i >= nkt_w) break;  // wave-uniform
+            if constexpr (A8) {
+                const uint8_t* xp = xs + (((xrow << a.nkt_shift) + i) << 7) + kq * 32;
+                const i32x8_t av = __builtin_bit_cast(
+                    i32x8_t, u32x8_cat(*reinterpret_cast<const u32x4_t*>(xp), *reinterpret_cast<const u32x4_t*>(xp + 16)));
+#pragma unroll
+                for (int sj = 0; sj < SG; ++sj) {
+                    const uint8_t* sp = ss + (((sj << a.nkt_shift) + i) * EB) + (SC == 2 ? 0 : col16 * (WIDE ? 4 : 2));
+                    const uint32_t bits = WIDE ? *reinterpret_cast<const uint32_t*>(sp)
+                                               : static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(sp));
+                    const float sc = scale_from_bits<WIDE>(bits, bf16_scale);
+                    const i32x8_t bv = __builtin_bit_cast(i32x8_t, u32x8_cat(wv[ii][sj][0], wv[ii][sj][NL - 1]));
+                    const f32x4_t part = mfma16x16x128_fp8(av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[sj][r] = __builtin_fmaf(sc, part[r], acc[sj][r]);
+                }
+                continue;
+            }
             u32x4_t xf[4];
             const uint8_t* xp = xs + (((xrow << a.nkt_shift) + i) << 8) + kq * 16;
 #pragma unroll
@@ -442,6 +476,15 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
                     }
                 }
             }
+        }
+    }
+
+    if constexpr (A8) {  // row scales (rows 4 kq + r; rows past M are never stored)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float sx = a.x_scale[min(4 * kq + r, a.m - 1)];
+#pragma unroll
+            for (int sj = 0; sj < SG; ++sj) acc[sj][r] *= sx;
         }
     }
 
@@ -585,23 +628,32 @@ void launch_decode_f(const decode_args& a, const decode_config& c, bool uniform,
 namespace {
 template <plm_format F, bool BF16, int SG, int NW, int CH>
 void launch_rr_t(const rr_args& a, int sc, int grid, size_t lds, hipStream_t s) {
+    if constexpr (F == PLM_FP8) {
+        if (a.xq != nullptr) {  // W8A8
+            if (sc == 0) decode_rr_kernel<F, BF16, SG, NW, CH, 0, true><<<grid, NW * 64, lds, s>>>(a);
+            else if (sc == 1) decode_rr_kernel<F, BF16, SG, NW, CH, 1, true><<<grid, NW * 64, lds, s>>>(a);
+            else decode_rr_kernel<F, BF16, SG, NW, CH, 2, true><<<grid, NW * 64, lds, s>>>(a);
+            return;
+        }
+    }
     if (sc == 0) decode_rr_kernel<F, BF16, SG, NW, CH, 0><<<grid, NW * 64, lds, s>>>(a);
     else if (sc == 1) decode_rr_kernel<F, BF16, SG, NW, CH, 1><<<grid, NW * 64, lds, s>>>(a);
     else decode_rr_kernel<F, BF16, SG, NW, CH, 2><<<grid, NW * 64, lds, s>>>(a);
 }
 template <plm_format F, bool BF16, int NW, int CH>
 void launch_rr_sg(const rr_args& a, int sc, int sg, size_t lds, hipStream_t s) {
-    const int grid = static_cast<int>(ceil_div(a.strips, sg));
-    switch (sg) {
-        case 1: launch_rr_t<F, BF16, 1, NW, CH>(a, sc, grid, lds, s); break;
-        case 2: launch_rr_t<F, BF16, 2, NW, CH>(a, sc, grid, lds, s); break;
-        case 3: launch_rr_t<F, BF16, 3, NW, CH>(a, sc, grid, lds, s); break;
-        default:
-            // fp8 tiles take twice the registers: at most three strips.
-            if constexpr (F == PLM_FP8) launch_rr_t<F, BF16, 3, NW, CH>(a, sc, static_cast<int>(ceil_div(a.strips, 3)), lds, s);
-            else if (sg == 4) launch_rr_t<F, BF16, 4, NW, CH>(a, sc, grid, lds, s);
-            else launch_rr_t<F, BF16, 6, NW, CH>(a, sc, grid, lds, s);
-            break;
+    if constexpr (F == PLM_FP8) {  // fp8 tiles and 4-tile batches: at most two strips
+        if (sg == 1) launch_rr_t<F, BF16, 1, NW, CH>(a, sc, a.strips, lds, s);
+        else launch_rr_t<F, BF16, 2, NW, CH>(a, sc, static_cast<int>(ceil_div(a.strips, 2)), lds, s);
+    } else {
+        const int grid = static_cast<int>(ceil_div(a.strips, sg));
+        switch (sg) {
+            case 1: launch_rr_t<F, BF16, 1, NW, CH>(a, sc, grid, lds, s); break;
+            case 2: launch_rr_t<F, BF16, 2, NW, CH>(a, sc, grid, lds, s); break;
+            case 3: launch_rr_t<F, BF16, 3, NW, CH>(a, sc, grid, lds, s); break;
+            case 4: launch_rr_t<F, BF16, 4, NW, CH>(a, sc, grid, lds, s); break;
+            default: launch_rr_t<F, BF16, 6, NW, CH>(a, sc, grid, lds, s); break;
+        }
     }
 }
 }  // namespace
@@ -697,7 +749,7 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
     const bool uniform = group_size % kTileK == 0;
     const int64_t tpg = group_size / kTileK;
     const int sc_mode = d.scale_cols == 16 ? (scale_dtype == PLM_FP32 ? 1 : 0) : (scale_dtype == PLM_FP32 ? 2 : -1);
-    if (uniform && (tpg & (tpg - 1)) == 0 && xq == nullptr && sc_mode >= 0 && !no_x_staging()) {
+    if (uniform && (tpg & (tpg - 1)) == 0 && sc_mode >= 0 && !no_x_staging()) {
         const rr_config rc = choose_rr(m, n, k);
         if (rc.sg > 0) {
             rr_args r{};
@@ -712,12 +764,14 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
             r.strips = static_cast<int>(d.strips);
             r.groups = static_cast<int>(d.groups);
             r.scale_dtype = scale_dtype;
+            r.xq = xq;
+            r.x_scale = x_scale;
             while ((int64_t{1} << r.tpg_shift) < tpg) ++r.tpg_shift;
             const int64_t nkt = ceil_div(d.ktiles, rc.nw);
             while ((int64_t{1} << r.nkt_shift) < nkt) ++r.nkt_shift;
             const int64_t slots = int64_t{1} << r.nkt_shift;
             const int eb = sc_mode == 0 ? 32 : (sc_mode == 1 ? 64 : 4);
-            r.x_bytes = static_cast<int>(round_up(m * slots * 256, 1024));
+            r.x_bytes = static_cast<int>(round_up(m * slots * (xq != nullptr ? kTileK : 2 * kTileK), 1024));
             // Scale copies write whole instructions: 64 lanes x (16 or 4) bytes.
             const int64_t cs = eb < 16 ? eb : 16;
             const int64_t s_bytes = round_up(rc.sg * slots * eb, 64 * cs);
@@ -725,7 +779,7 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
             const int64_t red = int64_t{rc.sg} * rc.nw * 64 * 16;
             const int64_t lds = std::max<int64_t>(int64_t{rc.nw} * r.wave_bytes, red);
             // One batch of loads per wavefront (CH tiles) keeps every load in flight at once.
-            const int64_t ch = rc.nw == 16 ? 2 : (f == PLM_INT4 ? 4 : 2);
+            const int64_t ch = f == PLM_FP8 ? 4 : (rc.nw == 16 ? 2 : 4);
             if (lds <= 160 * 1024 && slots <= ch) {
                 const size_t l = static_cast<size_t>(lds);
                 // CH: tiles per load batch (all of a wavefront's tiles at K = 4096).
@@ -738,12 +792,13 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
                         else launch_rr_sg<PLM_INT4, false, 8, 4>(r, sc_mode, rc.sg, l, s);
                     }
                 } else {
+                    // fp8 (K = 5120 at the Qwen3-27B shapes: 40 tiles, up to 3 per wavefront).
                     if (rc.nw == 16) {
-                        if (bf16) launch_rr_sg<PLM_FP8, true, 16, 2>(r, sc_mode, rc.sg, l, s);
-                        else launch_rr_sg<PLM_FP8, false, 16, 2>(r, sc_mode, rc.sg, l, s);
+                        if (bf16) launch_rr_sg<PLM_FP8, true, 16, 4>(r, sc_mode, rc.sg, l, s);
+                        else launch_rr_sg<PLM_FP8, false, 16, 4>(r, sc_mode, rc.sg, l, s);
                     } else {
-                        if (bf16) launch_rr_sg<PLM_FP8, true, 8, 2>(r, sc_mode, rc.sg, l, s);
-                        else launch_rr_sg<PLM_FP8, false, 8, 2>(r, sc_mode, rc.sg, l, s);
+                        if (bf16) launch_rr_sg<PLM_FP8, true, 8, 4>(r, sc_mode, rc.sg, l, s);
+                        else launch_rr_sg<PLM_FP8, false, 8, 4>(r, sc_mode, rc.sg, l, s);
                     }
                 }
                 PLM_HIP_LAUNCH_CHECK(op);
