@@ -94,3 +94,30 @@ def test_config5_t4096_sample():
     sample = np.random.default_rng(0).choice(t, 64, replace=False)
     ref = O.routed_experts_ref(h[sample], experts[sample], weights[sample], gu[2], dn[2])
     assert_moe_close(out[torch.from_numpy(sample).cuda()], ref, "moe t=4096 sample")
+
+
+def test_routed_experts_graph_replays_match_eager():
+    """The whole block (sort, tile lists, a two-level plan since rows >= 128 per expert,
+    activation, combine) captured into a graph: every replay must equal the eager result,
+    with eager work between replays (no node may depend on state left by the capture)."""
+    t, e, hidden, inter, top_k, g = 1024, 8, 256, 128, 2, 128
+    h, experts, weights, gu, dn = _moe_case(t, e, hidden, inter, top_k, g, seed=77)
+    hd, ed, wd = to_dev(h, torch.bfloat16), to_dev(experts.astype(np.int32)), to_dev(weights)
+    eager, _ = ops.routed_experts_int4_cuda(hd, ed, wd, gu[:2], dn[:2], inter, g)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        ops.routed_experts_int4_cuda(hd, ed, wd, gu[:2], dn[:2], inter, g)  # first-call set-up outside capture
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out, _ = ops.routed_experts_int4_cuda(hd, ed, wd, gu[:2], dn[:2], inter, g)
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs from the eager result"
+        again, _ = ops.routed_experts_int4_cuda(hd, ed, wd, gu[:2], dn[:2], inter, g)
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)
+    ref = O.routed_experts_ref(h, experts, weights, gu[2], dn[2])
+    assert_moe_close(out, ref, "moe graph t=1024")
