@@ -299,3 +299,16 @@ def test_decode_small_k_and_narrow_n(m, n, k, g):
     x = x_case(m, k, "bf16", seed=m)
     y = ops.gemm_int4_marlin_cuda(to_dev(x, torch.bfloat16), w, sc, n, 1, g)
     assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, g), None), f"m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 4])
+@pytest.mark.parametrize("n,k,g,dtype", [(4096, 12288, 128, "bf16"), (520, 10240, 128, "bf16"),
+                                         (264, 16384, 256, "fp16"), (100, 12288, 128, "fp16")])
+def test_decode_long_k(m, n, k, g, dtype):
+    """M <= 4 at long K (80-128 K tiles, more than the round-robin kernel's one load batch
+    holds): the split-K decode kernel, with 128- and 256-wide groups, fp16 x and ragged N."""
+    packed, s = int4_case(n, k, g, 1, seed=n + k + m)
+    w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), scale_tensor(s), 1, g)
+    x = x_case(m, k, dtype, seed=m + 3)
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, TDT[dtype]), w, sc, n, 1, g)
+    assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, g, dtype), None), f"m={m} n={n} k={k} g={g}")
