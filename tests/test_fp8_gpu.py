@@ -15,8 +15,11 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
-@pytest.mark.parametrize("m,k", [(1, 128), (16, 5120), (37, 1040)])
+@pytest.mark.parametrize("m,k", [(1, 128), (16, 5120), (37, 1040), (3, 1044), (2, 40000), (600, 17408), (520, 96)])
 def test_quantize_rows_bit_exact(m, k, dtype):
+    """Rows of 8-value chunks take the vectorised kernel (1024 threads a row below 512 rows,
+    256 above; K = 40000 and 17408 also exercise the chunks read twice); K = 1044 (not a
+    multiple of 8) takes the scalar kernel."""
     rng = np.random.default_rng(m + k)
     x = O.round_to(rng.standard_normal((m, k)).astype(np.float32) * np.exp2(rng.integers(-6, 6, (m, 1))), dtype)
     x[0, :3] = 0.0
