@@ -15,6 +15,7 @@
 // * the scatter-back is a gather: each token sums its top_k weighted expert outputs in k
 //   order in fp32 and rounds once, so the result does not depend on scheduling.
 #include <algorithm>
+#include <cstdlib>
 
 #include "plm_common.hpp"
 
@@ -148,6 +149,128 @@ __global__ void __launch_bounds__(1024) moe_tiles_kernel(const int32_t* __restri
         }
     }
     for (int64_t t = n_tiles + threadIdx.x; t < max_tiles; t += blockDim.x) {
+        tiles[3 * t] = 0;
+        tiles[3 * t + 1] = 0;
+        tiles[3 * t + 2] = 0;
+    }
+}
+
+// Sort, offsets and single-level tile list in one workgroup, for small batches: the same
+// results as moe_hist/scan/scatter/tiles above (a stable sort by expert), in one launch
+// instead of five. The assignments are split into 64-row chunks; the wavefront that owns a
+// chunk ranks each assignment among the chunk's earlier ones with the same expert (a ballot
+// per distinct expert) and writes the per-(expert, chunk) count into an expert-major LDS
+// table. One exclusive scan of that table gives each (expert, chunk) its first sorted row,
+// so an assignment's row is that base plus its rank.
+constexpr int kSmallSortTable = 16384;  // experts x chunks held in LDS
+constexpr int kSmallSortChunks = 128;   // chunks (8 per wavefront), so rows <= 8192
+
+__global__ void __launch_bounds__(1024) moe_sort_small_kernel(
+    const int32_t* __restrict__ experts, const float* __restrict__ weights, int rows, int top_k, int n_experts,
+    int n_chunks, int bm, int64_t max_tiles, int32_t* __restrict__ sorted_token, float* __restrict__ sorted_weight,
+    int32_t* __restrict__ position, int32_t* __restrict__ offsets, int32_t* __restrict__ tiles) {
+    __shared__ int32_t tab[kSmallSortTable];
+    __shared__ int32_t buf[1024];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = n_experts * n_chunks;
+    for (int i = tid; i < n; i += 1024) tab[i] = 0;
+    __syncthreads();
+
+    constexpr int kPerWave = kSmallSortChunks / 16;
+    const uint64_t lanes_below = (uint64_t{1} << lane) - 1;
+    int ex[kPerWave], rk[kPerWave];
+#pragma unroll
+    for (int j = 0; j < kPerWave; ++j) {
+        const int c = wave + 16 * j;
+        const int a = c * 64 + lane;
+        int e = (c < n_chunks && a < rows) ? experts[a] : -1;
+        if (e >= n_experts) e = -1;  // out-of-range experts are skipped, as by the histogram
+        uint64_t todo = __ballot(e >= 0);
+        int rank = 0;
+        while (todo != 0) {  // wave-uniform: one pass per distinct expert in the chunk
+            const int leader = __ffsll(static_cast<unsigned long long>(todo)) - 1;
+            const int v = __shfl(e, leader);
+            const uint64_t same = __ballot(e == v) & todo;
+            if (e == v) rank = __popcll(same & lanes_below);
+            if (lane == leader) tab[v * n_chunks + c] = __popcll(same);
+            todo &= ~same;
+        }
+        ex[j] = e;
+        rk[j] = rank;
+    }
+    __syncthreads();
+
+    // Exclusive scan of tab: P consecutive entries per thread, then across threads.
+    const int per = (n + 1023) / 1024;
+    int32_t local = 0;
+    for (int q = 0; q < per; ++q) {
+        const int i = tid * per + q;
+        if (i < n) local += tab[i];
+    }
+    buf[tid] = local;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1) {
+        const int32_t y = tid >= d ? buf[tid - d] : 0;
+        __syncthreads();
+        buf[tid] += y;
+        __syncthreads();
+    }
+    const int32_t total = buf[1023];
+    int32_t run = buf[tid] - local;
+    for (int q = 0; q < per; ++q) {
+        const int i = tid * per + q;
+        if (i < n) {
+            const int32_t v = tab[i];
+            tab[i] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+
+    // Inclusive-end offsets (the next expert's first row), and each expert's tile count.
+    constexpr int kExpertsPerThread = 4096 / 1024;
+    int32_t lo[kExpertsPerThread], hi[kExpertsPerThread];
+#pragma unroll
+    for (int q = 0; q < kExpertsPerThread; ++q) {
+        const int e = tid + 1024 * q;
+        lo[q] = hi[q] = 0;
+        if (e < n_experts) {
+            lo[q] = tab[e * n_chunks];
+            hi[q] = e + 1 < n_experts ? tab[(e + 1) * n_chunks] : total;
+            offsets[e] = hi[q];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kPerWave; ++j) {
+        if (ex[j] < 0) continue;
+        const int c = wave + 16 * j;
+        const int a = c * 64 + lane;
+        const int32_t pos = tab[ex[j] * n_chunks + c] + rk[j];
+        sorted_token[pos] = a / top_k;
+        sorted_weight[pos] = weights[a];
+        position[a] = pos;
+    }
+    __syncthreads();  // tab is reused for the tile prefix below
+
+#pragma unroll
+    for (int q = 0; q < kExpertsPerThread; ++q) {
+        const int e = tid + 1024 * q;
+        if (e < n_experts) tab[e] = (hi[q] - lo[q] + bm - 1) / bm;
+    }
+    __syncthreads();
+    const int32_t n_tiles = block_exclusive_scan(tab, n_experts, buf);
+#pragma unroll
+    for (int q = 0; q < kExpertsPerThread; ++q) {
+        const int e = tid + 1024 * q;
+        if (e >= n_experts) continue;
+        int32_t t = tab[e];
+        for (int32_t r = lo[q]; r < hi[q]; r += bm, ++t) {
+            tiles[3 * t] = e;
+            tiles[3 * t + 1] = r;
+            tiles[3 * t + 2] = min(bm, hi[q] - r);
+        }
+    }
+    for (int64_t t = n_tiles + tid; t < max_tiles; t += 1024) {
         tiles[3 * t] = 0;
         tiles[3 * t + 1] = 0;
         tiles[3 * t + 2] = 0;
@@ -316,6 +439,14 @@ grouped_plan plan_grouped(int64_t rows, int64_t n_experts) {
     return p;
 }
 
+bool small_sort_enabled() {
+    static const bool on = [] {
+        const char* e = getenv("PLM_MOE_SMALL_SORT");  // "0": always the multi-kernel sort (A/B)
+        return e == nullptr || e[0] != '0';
+    }();
+    return on;
+}
+
 int64_t moe_max_tiles(int64_t rows, int64_t n_experts) { return plan_grouped(rows, n_experts).slots(); }
 
 int launch_sort(const char* op, const int32_t* experts, const float* weights, int64_t rows, int64_t top_k,
@@ -441,8 +572,18 @@ int plm_moe(const void* h, plm_dtype dtype, const int32_t* top_experts, const fl
     hipStream_t s = as_stream(stream);
     const bool bf16 = dtype == PLM_BF16;
     auto* tiles = reinterpret_cast<int32_t*>(base + l.tiles);
-    if (int rc = launch_sort(op, top_experts, top_weights, rows, top_k, n_experts, base, l, offsets, s)) return rc;
-    if (int rc = launch_tiles(op, offsets, n_experts, p, tiles, s)) return rc;
+    const int64_t chunks64 = ceil_div(rows, 64);
+    if (!p.two && chunks64 <= kSmallSortChunks && n_experts * chunks64 <= kSmallSortTable && small_sort_enabled()) {
+        moe_sort_small_kernel<<<1, 1024, 0, s>>>(
+            top_experts, top_weights, int(rows), int(top_k), int(n_experts), int(chunks64),
+            grouped_block_rows(p.shape), p.max_a, reinterpret_cast<int32_t*>(base + l.sorted_token),
+            reinterpret_cast<float*>(base + l.sorted_weight), reinterpret_cast<int32_t*>(base + l.position), offsets,
+            tiles);
+        PLM_HIP_LAUNCH_CHECK(op);
+    } else {
+        if (int rc = launch_sort(op, top_experts, top_weights, rows, top_k, n_experts, base, l, offsets, s)) return rc;
+        if (int rc = launch_tiles(op, offsets, n_experts, p, tiles, s)) return rc;
+    }
     // gate_up: [rows, 2I] = h[sorted_token] @ gate_up_e^T
     if (int rc = launch_plan(op, p, h, bf16, gate_up_weight, gate_up_scale, scale_dtype, rows, 2 * intermediate,
                              hidden, 1, group_size, base + l.gu, tiles,
