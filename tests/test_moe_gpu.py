@@ -9,7 +9,7 @@ import torch
 
 from oracle import oracle as O
 from pulsarlm_amd import ops
-from tests._util import assert_close, to_dev, to_np
+from tests._util import TDT, assert_close, to_dev, to_np
 
 
 def assert_moe_close(y, ref, what):
@@ -25,13 +25,22 @@ def assert_moe_close(y, ref, what):
 pytestmark = pytest.mark.gpu
 
 
-def _experts(e, n, k, g, seed):
+def _experts(e, n, k, g, seed, scale_dtype="fp16", x_dtype="bf16"):
     rng = np.random.default_rng(seed)
     q = rng.integers(-8, 8, size=(e, n, k))
     packed = np.stack([O.pack_int4(q[i]) for i in range(e)])
-    scale = (np.abs(rng.standard_normal((e, n, k // g)) * 0.02) + 1e-3).astype(np.float16)
-    w, s = ops.repack_int4_experts(to_dev(packed), to_dev(scale), g)
-    deq = np.stack([O.dequant_int4(packed[i], scale[i], 1, g) for i in range(e)])
+    scale = np.abs(rng.standard_normal((e, n, k // g)) * 0.02) + 1e-3
+    if scale_dtype == "fp16":
+        scale = scale.astype(np.float16)
+        s_dev = to_dev(scale)
+    elif scale_dtype == "fp32":
+        scale = scale.astype(np.float32)
+        s_dev = to_dev(scale)
+    else:  # bf16-stored scales
+        scale = O.round_to(scale.astype(np.float32), "bf16")
+        s_dev = to_dev(scale).to(torch.bfloat16)
+    w, s = ops.repack_int4_experts(to_dev(packed), s_dev, g)
+    deq = np.stack([O.dequant_int4(packed[i], scale[i], 1, g, x_dtype) for i in range(e)])
     return w, s, deq
 
 
@@ -57,6 +66,26 @@ def test_grouped_gemm_matches_per_expert_reference(counts):
             ref[start:end] = O.gemm_ref(x[start:end], deq[i], None)
         start = end
     assert_close(y, ref, f"grouped {counts}")
+
+
+# The 16-row grouped tiles (few rows per expert) across scale storage, activation dtype and
+# 256-wide groups, with an expert spanning several tiles and a ragged N.
+@pytest.mark.parametrize("sdt,xdt,g", [("fp32", "bf16", 128), ("bf16", "fp16", 128), ("fp16", "fp16", 256)])
+def test_grouped_decode_path(sdt, xdt, g):
+    counts = [70, 0, 3, 1, 0, 0, 20, 2, 33, 0, 0, 64]
+    e, n, k = len(counts), 200, 1536
+    w, s, deq = _experts(e, n, k, g, seed=11, scale_dtype=sdt, x_dtype=xdt)
+    rows = sum(counts)
+    x = O.round_to(np.random.default_rng(3).standard_normal((rows, k)).astype(np.float32), xdt)
+    offsets = np.cumsum(counts).astype(np.int32)
+    y = ops.grouped_gemm_int4_cuda(to_dev(x, TDT[xdt]), w, s, to_dev(offsets), n, g)
+    ref = np.zeros((rows, n), np.float32)
+    start = 0
+    for i, end in enumerate(offsets):
+        if end > start:
+            ref[start:end] = O.gemm_ref(x[start:end], deq[i], None)
+        start = end
+    assert_close(y, ref, f"grouped decode {sdt} {xdt} g={g}")
 
 
 def _moe_case(t, e, hidden, inter, top_k, g, seed):
