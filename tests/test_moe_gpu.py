@@ -71,7 +71,7 @@ def test_grouped_gemm_matches_per_expert_reference(counts):
 # The 16-row grouped tiles (few rows per expert) across scale storage, activation dtype and
 # 256-wide groups, with an expert spanning several tiles and a ragged N.
 @pytest.mark.parametrize("sdt,xdt,g", [("fp32", "bf16", 128), ("bf16", "fp16", 128), ("fp16", "fp16", 256)])
-def test_grouped_decode_path(sdt, xdt, g):
+def test_grouped_small_tiles(sdt, xdt, g):
     counts = [70, 0, 3, 1, 0, 0, 20, 2, 33, 0, 0, 64]
     e, n, k = len(counts), 200, 1536
     w, s, deq = _experts(e, n, k, g, seed=11, scale_dtype=sdt, x_dtype=xdt)
@@ -85,7 +85,7 @@ def test_grouped_decode_path(sdt, xdt, g):
         if end > start:
             ref[start:end] = O.gemm_ref(x[start:end], deq[i], None)
         start = end
-    assert_close(y, ref, f"grouped decode {sdt} {xdt} g={g}")
+    assert_close(y, ref, f"grouped 16-row tiles {sdt} {xdt} g={g}")
 
 
 def _moe_case(t, e, hidden, inter, top_k, g, seed):
