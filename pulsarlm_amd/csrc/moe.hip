@@ -158,10 +158,10 @@ __global__ void __launch_bounds__(1024) moe_tiles_kernel(const int32_t* __restri
 // Sort, offsets and single-level tile list in one workgroup, for small batches: the same
 // results as moe_hist/scan/scatter/tiles above (a stable sort by expert), in one launch
 // instead of five. The assignments are split into 64-row chunks; the wavefront that owns a
-// chunk ranks each assignment among the chunk's earlier ones with the same expert (a ballot
-// per distinct expert) and writes the per-(expert, chunk) count into an expert-major LDS
-// table. One exclusive scan of that table gives each (expert, chunk) its first sorted row,
-// so an assignment's row is that base plus its rank.
+// chunk ranks each assignment among the chunk's earlier ones with the same expert (one
+// ballot per bit of the expert id) and writes the per-(expert, chunk) count into an
+// expert-major LDS table. One exclusive scan of that table gives each (expert, chunk) its
+// first sorted row, so an assignment's row is that base plus its rank.
 constexpr int kSmallSortTable = 16384;  // experts x chunks held in LDS
 constexpr int kSmallSortChunks = 128;   // chunks (8 per wavefront), so rows <= 8192
 
@@ -179,22 +179,36 @@ __global__ void __launch_bounds__(1024) moe_sort_small_kernel(
     constexpr int kPerWave = kSmallSortChunks / 16;
     const uint64_t lanes_below = (uint64_t{1} << lane) - 1;
     int ex[kPerWave], rk[kPerWave];
+    float wt[kPerWave];
+#pragma unroll
+    for (int j = 0; j < kPerWave; ++j) {  // all loads first: one latency, not one per chunk
+        const int c = wave + 16 * j;
+        const int a = c * 64 + lane;
+        const bool in = c < n_chunks && a < rows;
+        ex[j] = in ? experts[a] : -1;
+        wt[j] = in ? weights[a] : 0.f;
+    }
+    // Lanes with the same expert: AND over the expert id's bits of that bit's ballot or its
+    // complement (one ballot per bit instead of one pass per distinct expert).
+    const int id_bits = 32 - __clz(max(n_experts - 1, 1));
 #pragma unroll
     for (int j = 0; j < kPerWave; ++j) {
         const int c = wave + 16 * j;
-        const int a = c * 64 + lane;
-        int e = (c < n_chunks && a < rows) ? experts[a] : -1;
+        int e = ex[j];
         if (e >= n_experts) e = -1;  // out-of-range experts are skipped, as by the histogram
-        uint64_t todo = __ballot(e >= 0);
-        int rank = 0;
-        while (todo != 0) {  // wave-uniform: one pass per distinct expert in the chunk
-            const int leader = __ffsll(static_cast<unsigned long long>(todo)) - 1;
-            const int v = __shfl(e, leader);
-            const uint64_t same = __ballot(e == v) & todo;
-            if (e == v) rank = __popcll(same & lanes_below);
-            if (lane == leader) tab[v * n_chunks + c] = __popcll(same);
-            todo &= ~same;
+        uint64_t same = __ballot(e >= 0);
+        if (same == 0) {  // wave-uniform: no assignment in this chunk
+            ex[j] = -1;
+            rk[j] = 0;
+            continue;
         }
+        for (int b = 0; b < id_bits; ++b) {  // wave-uniform
+            const bool bit = (e >> b) & 1;
+            const uint64_t plane = __ballot(bit);
+            same &= bit ? plane : ~plane;
+        }
+        const int rank = __popcll(same & lanes_below);
+        if (e >= 0 && rank == 0) tab[e * n_chunks + c] = __popcll(same);
         ex[j] = e;
         rk[j] = rank;
     }
@@ -247,7 +261,7 @@ __global__ void __launch_bounds__(1024) moe_sort_small_kernel(
         const int a = c * 64 + lane;
         const int32_t pos = tab[ex[j] * n_chunks + c] + rk[j];
         sorted_token[pos] = a / top_k;
-        sorted_weight[pos] = weights[a];
+        sorted_weight[pos] = wt[j];
         position[a] = pos;
     }
     __syncthreads();  // tab is reused for the tile prefix below

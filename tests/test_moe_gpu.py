@@ -100,7 +100,7 @@ def _moe_case(t, e, hidden, inter, top_k, g, seed):
                                                    (16, 1024, 128, 128, 8), (1024, 128, 256, 128, 8),
                                                    (70, 3, 128, 128, 3)])
 def test_routed_experts_matches_oracle(t, e, hidden, inter, top_k):
-    """Up to 8192 rows with one tile shape, the sort runs as one workgroup (a ballot rank per
+    """Up to 8192 rows with one tile shape, the sort runs as one workgroup (a ballot-plane rank per
     64-row chunk and a scan of the experts x chunks table); 1024 x 128 fills that table,
     and 16 x 1024 spreads few rows over many experts."""
     g = 128
