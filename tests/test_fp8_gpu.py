@@ -66,6 +66,22 @@ def test_config4_qwen3_27b_shapes(shape, m):
     assert_close(y8[rows], O.gemm_w8a8_ref(xc, xs, codes, scale, 128, 128, dtype=None), f"w8a8 {shape} m={m}")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("m", [1, 4, 16, 17, 100, 300])
+def test_w8a16_32x32_blocks(m, dtype):
+    """The reference's model-level fp8 configuration (test_qwen3_5.cpp:691-696): 32 x 32
+    quantization blocks, so block_n = 32 (one scale per two 16-column strips) and 32-wide
+    scale groups (four per 128-wide K tile), through the decode and MFMA kernels."""
+    n, k = 200, 416
+    rng = np.random.default_rng(m)
+    w = O.bf16_round(rng.standard_normal((n, k)).astype(np.float32) * 0.02)
+    codes, scale = O.fp8_block_quantize(w, 32, 32)
+    wt, st = ops.repack_fp8_marlin_cuda(to_dev(codes).view(torch.float8_e4m3fn), to_dev(scale), 32, 32)
+    x = O.round_to(rng.standard_normal((m, k)).astype(np.float32), dtype)
+    y = ops.gemm_fp8_marlin_cuda(to_dev(x, TDT[dtype]), wt, st, n, 32, 32)
+    assert_close(y, O.gemm_ref(x, O.dequant_fp8(codes, scale, 32, 32, dtype), None), f"fp8 32x32 m={m}")
+
+
 def test_w8a8_rejects_small_groups():
     codes = np.zeros((64, 256), np.uint8)
     wt, st = ops.repack_fp8_marlin_cuda(to_dev(codes).view(torch.float8_e4m3fn),
