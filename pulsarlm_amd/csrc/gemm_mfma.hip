@@ -79,7 +79,11 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     constexpr int SLOTS = a_traits<A8>::slots;
     constexpr int RPC = 1024 / ARB;  // A rows per 1 KiB chunk
     constexpr int A_STAGE = BM * ARB;
-    constexpr int B_STAGE = BS * TB;
+    // fp8 W8A16 with one row of wavefronts: no two wavefronts share a weight strip, so each
+    // loads its own strips' tiles for the next K step into registers and LDS holds only x
+    // (the 2 KiB fp8 tiles of 16 strips would not fit beside two 64 KiB x stages).
+    constexpr bool BREG = F == PLM_FP8 && !A8 && !GROUPED && WM == 1;
+    constexpr int B_STAGE = BREG ? 0 : BS * TB;
     constexpr int STAGE = A_STAGE + B_STAGE;
     constexpr int A_CHUNKS = A_STAGE / 1024, B_CHUNKS = B_STAGE / 1024;
     constexpr int A_PW = (A_CHUNKS + NW - 1) / NW;  // 1 KiB chunks each wavefront loads per K step
@@ -165,13 +169,20 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     const __amdgpu_buffer_rsrc_t b_rsrc =
         make_rsrc(wbase + static_cast<int64_t>(strip0) * strip_bytes,
                   static_cast<uint32_t>(min(BS, a.strips - strip0) * strip_bytes));
-    int b_off[B_PW];
+    int b_off[B_PW > 0 ? B_PW : 1];
 #pragma unroll
     for (int i = 0; i < B_PW; ++i) {
         const int c = wave * B_PW + i;
         b_off[i] = (c / (TB / 1024)) * strip_bytes + (c % (TB / 1024)) * 1024 + lane * 16;
     }
 
+    auto load_breg = [&](u32x4_t (&dst)[NS][TB / 1024], int kt) {
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+#pragma unroll
+            for (int h = 0; h < TB / 1024; ++h)
+                dst[j][h] = buffer_load16(b_rsrc, (wn * NS + j) * strip_bytes + h * 1024 + lane * 16, kt * TB);
+    };
     auto issue = [&](int kt, int stage) {
         uint8_t* sa = lds + stage * STAGE;
 #pragma unroll
@@ -208,12 +219,14 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         for (int j = 0; j < NS; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     uint32_t sc[NS][ST];
+    u32x4_t wreg[NS][TB / 1024], wnext[NS][TB / 1024];  // BREG: this and the next step's tiles
     if (kt_begin < kt_end) {
 #pragma unroll
         for (int j = 0; j < NS; ++j)
 #pragma unroll
             for (int t = 0; t < ST; ++t) sc[j][t] = scale_bits(j, kt_begin, t);
         issue(kt_begin, 0);
+        if constexpr (BREG) load_breg(wreg, kt_begin);
     }
 
     for (int kt = kt_begin; kt < kt_end; ++kt) {
@@ -230,6 +243,7 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
 #pragma unroll
                 for (int t = 0; t < ST; ++t) scn[j][t] = scale_bits(j, kt + 1, t);
             issue(kt + 1, stage ^ 1);
+            if constexpr (BREG) load_breg(wnext, kt + 1);
         }
 
         const uint8_t* sa = lds + stage * STAGE;
@@ -239,7 +253,8 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         for (int j = 0; j < NS; ++j)
 #pragma unroll
             for (int h = 0; h < TB / 1024; ++h)
-                wv[j][h] = *reinterpret_cast<const u32x4_t*>(sb + (wn * NS + j) * TB + h * 1024 + lane * 16);
+                wv[j][h] = BREG ? wreg[j][h]
+                                : *reinterpret_cast<const u32x4_t*>(sb + (wn * NS + j) * TB + h * 1024 + lane * 16);
 
         if constexpr (A8) {
 #pragma unroll
@@ -286,6 +301,12 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
             for (int j = 0; j < NS; ++j)
 #pragma unroll
                 for (int t = 0; t < ST; ++t) sc[j][t] = scn[j][t];
+            if constexpr (BREG) {
+#pragma unroll
+                for (int j = 0; j < NS; ++j)
+#pragma unroll
+                    for (int h = 0; h < TB / 1024; ++h) wreg[j][h] = wnext[j][h];
+            }
         }
     }
 
@@ -392,6 +413,7 @@ bool no_tail() {
 // (W8A8): with bf16 x and 2 KiB fp8 tiles two stages would not fit the 160 KiB LDS.
 mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) {
     const bool wide_ok = f == PLM_INT4 || a8;
+    const bool tall_ok = wide_ok || f == PLM_FP8;  // fp8 W8A16 runs the tall shape with weights in registers
     const int64_t cus = cu_count();
     const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
     auto config = [&](int id) {
@@ -419,8 +441,12 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
     auto cost = [&](const mfma_config& c) {
         const shape sh = shape_of(c.shape);
         // fp8 W8A16 (2 KiB weight tiles dequantized to bf16): 128 x 128 measured 10-15 %
-        // slower than 256 x 128 at the Qwen3-27B shapes, unlike int4.
-        const double rate = f == PLM_FP8 && !a8 && c.shape == 0 ? 0.5 : kShapeRate[c.shape];
+        // slower than 256 x 128 at the Qwen3-27B shapes, unlike int4; the tall shape (weights
+        // in registers) measured 15 % faster than 256 x 128 for gate_up (1088 tiles) and slower
+        // for the layers with 160-448 tiles, which a rate of 0.75 reproduces.
+        double rate = kShapeRate[c.shape];
+        if (f == PLM_FP8 && !a8 && c.shape == 0) rate = 0.5;
+        if (f == PLM_FP8 && !a8 && c.shape == 6) rate = 0.75;
         const double area = static_cast<double>(sh.bm()) * sh.bs() / rate;
         const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
         if (c.tail_tiles > 0) {
@@ -435,11 +461,11 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
     };
     if (const char* env = getenv("PLM_MFMA")) {  // tuning sweeps: S, L, H or R
         const int id = env[0] == 'X' ? 6 : env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
-        return config((id == 2 || id >= 5) && !wide_ok ? 1 : id);
+        return config(((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok) ? 1 : id);
     }
     mfma_config best = config(0);
     for (int id : {1, 2, 3, 5, 6}) {
-        if ((id == 2 || id >= 5) && !wide_ok) continue;
+        if (((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok)) continue;
         const mfma_config c = config(id);
         if (cost(c) < cost(best)) best = c;
     }
@@ -458,6 +484,13 @@ int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k, bool
 namespace {
 template <plm_format F, bool BF16, bool UNIFORM, bool WIDE, bool A8, bool GROUPED>
 void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
+    if constexpr (F == PLM_FP8 && !A8 && !GROUPED) {  // weights in registers (BREG): tall only
+        if (shape == 6) {
+            mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kTall.wm, kTall.wn, kTall.mt, kTall.ns>
+                <<<grid, kTall.wm * kTall.wn * 64, 0, s>>>(a);
+            return;
+        }
+    }
     if constexpr (((F == PLM_INT4 && !A8) || (F == PLM_FP8 && A8)) && !GROUPED) {
         if (shape == 2) {
             mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kHuge.wm, kHuge.wn, kHuge.mt, kHuge.ns>
