@@ -22,7 +22,7 @@ present. ``cpu_baseline`` times the oracle's dequantize-then-matmul (numpy, all
 host cores) on config 1.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
-       [--only decode|prefill|fp8|moe] [--eager] [--no-cpu]
+       [--only decode|prefill|fp8|moe|copy|crossover [--m 1,2,...]] [--eager] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -63,7 +63,8 @@ def parse():
     p.add_argument("--steps", type=int, default=24)
     p.add_argument("--warmup", type=int, default=6)
     p.add_argument("--quick", action="store_true", help="decode headline only")
-    p.add_argument("--only", choices=["decode", "prefill", "fp8", "moe", "copy"], default=None)
+    p.add_argument("--only", choices=["decode", "prefill", "fp8", "moe", "copy", "crossover"], default=None)
+    p.add_argument("--m", default="1,2,4,8,12,16,24,32,48,64", help="M values of --only crossover")
     p.add_argument("--eager", action="store_true", help="no graphs (for profiler attribution)")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-detail", action="store_true", help="headline step only (profiler runs)")
@@ -287,6 +288,30 @@ def section_moe(b: Bench):
     return out
 
 
+def section_crossover(b: Bench, ms):
+    """The decode kernel against the MFMA kernel around M = 16 (o and gate_up, int4 g128):
+    run once as is and once with PLM_DECODE_MAX_M=0 (every M on the MFMA kernel)."""
+    torch, L = b.torch, b._lib
+    limit = int(os.environ.get("PLM_DECODE_MAX_M", "16"))
+    out = {"decode_max_m": limit}
+    for i, (name, k, n) in enumerate(SHAPES):
+        if name not in ("o", "gate_up"):
+            continue
+        copies = b.int4_layer(k, n, i, min_copies=2)
+        for m in ms:
+            x = torch.randn(m, k, device=b.dev).to(torch.bfloat16)
+            y = torch.empty(m, n, device=b.dev, dtype=torch.bfloat16)
+            launches = [b.gemm_launch(L.PLM_INT4, x, w, s, L.PLM_FP16, m, n, k, 1, y) for (w, s) in copies]
+            tt = b.time(launches, reps=5) / len(copies)
+            gbs = w4a16_bytes(m, n, k) / tt / 1e9
+            tf = 2 * m * n * k / tt / 1e12
+            out[f"{name}_m{m}"] = {"kernel": "decode" if m <= min(limit, 16) else "mfma", "us": round(tt * 1e6, 2),
+                                   "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3),
+                                   "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+        del copies
+    return out
+
+
 def section_copy(b: Bench):
     """A plain device copy of known size: the calibration run for the FETCH_SIZE /
     WRITE_SIZE counters (their reading for 256 MiB read + 256 MiB written)."""
@@ -312,7 +337,9 @@ def main():
     torch.manual_seed(0)
     b = Bench(args.eager)
     if args.only and args.only != "decode":
-        fn = {"prefill": section_prefill, "fp8": section_fp8, "moe": section_moe, "copy": section_copy}[args.only]
+        ms = [int(v) for v in args.m.split(",")]
+        fn = {"prefill": section_prefill, "fp8": section_fp8, "moe": section_moe, "copy": section_copy,
+              "crossover": lambda b_: section_crossover(b_, ms)}[args.only]
         print(json.dumps({args.only: fn(b)}))
         return
 

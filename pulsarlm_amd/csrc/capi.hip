@@ -3,6 +3,7 @@
 // kernel (M <= 16, the reference's small_m switch at marlin.cu:577) and the MFMA
 // kernel.
 #include <algorithm>
+#include <cstdlib>
 
 #include "plm_common.hpp"
 
@@ -19,7 +20,16 @@ int launch_quantize_rows(const char* op, const void* x, bool bf16, int64_t m, in
 int64_t decode_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k);
 int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k, bool a8);
 
-constexpr int64_t kDecodeMaxM = 16;
+// Largest M served by the decode kernels (their MFMA tiles hold 16 rows); above it the MFMA
+// kernel runs. Environment PLM_DECODE_MAX_M (0-16) lowers it, for measuring one path
+// against the other at the same M.
+int64_t decode_max_m() {
+    static const int64_t v = [] {
+        const char* e = getenv("PLM_DECODE_MAX_M");
+        return e == nullptr ? int64_t{16} : std::min<int64_t>(16, std::max<int64_t>(0, atoll(e)));
+    }();
+    return v;
+}
 
 const char* gemm_op_name(plm_format f) { return f == PLM_INT4 ? "gemm_int4_marlin" : "gemm_fp8_marlin"; }
 
@@ -53,7 +63,7 @@ extern "C" {
 
 int64_t plm_gemm_workspace_bytes(plm_format format, int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0) return 0;
-    return m <= kDecodeMaxM ? decode_workspace_bytes(format, m, n, k) : mfma_workspace_bytes(format, m, n, k, false);
+    return m <= decode_max_m() ? decode_workspace_bytes(format, m, n, k) : mfma_workspace_bytes(format, m, n, k, false);
 }
 
 int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype, const void* weight, const void* scale,
@@ -65,7 +75,7 @@ int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype, const void* we
         return rc;
     if (m == 0 || n == 0) return PLM_OK;
     const bool bf16 = x_dtype == PLM_BF16;
-    if (m <= kDecodeMaxM)
+    if (m <= decode_max_m())
         return launch_decode(op, format, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y,
                              workspace, workspace_bytes, as_stream(stream), nullptr, nullptr);
     return launch_mfma(op, format, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, workspace,
@@ -84,7 +94,7 @@ w8a8_ws w8a8_layout(int64_t m, int64_t n, int64_t k) {
     w8a8_ws w{};
     // The split-K counters always keep the front of the workspace, even when this call
     // does not split, so scratch written here never lands on them.
-    const int64_t gemm = m <= kDecodeMaxM ? decode_workspace_bytes(PLM_FP8, m, n, k) : mfma_workspace_bytes(PLM_FP8, m, n, k, true);
+    const int64_t gemm = m <= decode_max_m() ? decode_workspace_bytes(PLM_FP8, m, n, k) : mfma_workspace_bytes(PLM_FP8, m, n, k, true);
     w.gemm = round_up(std::max<int64_t>(gemm, kCounterBytes), 256);
     w.xq = round_up(m * ceil_div(k, kTileK) * kTileK, 256);
     w.sx = round_up(m * 4, 256);
@@ -133,7 +143,7 @@ int plm_gemm_w8a8(const void* x, plm_dtype x_dtype, const void* weight, const vo
     const bool bf16 = x_dtype == PLM_BF16;
     hipStream_t s = as_stream(stream);
     if (int rc = launch_quantize_rows(op, x, bf16, m, k, xq, sx, true, s)) return rc;
-    if (m <= kDecodeMaxM)
+    if (m <= decode_max_m())
         return launch_decode(op, PLM_FP8, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, base,
                              static_cast<size_t>(l.gemm), s, xq, sx);
     return launch_mfma(op, PLM_FP8, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, base,
