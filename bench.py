@@ -18,8 +18,8 @@ MoE block at T = 256 / 4096 (config 5).
 algorithmic bytes per launch / average launch time from HIP events around the
 graph replays on the launch stream; ``traffic`` comes from the committed
 rocprofv3 FETCH_SIZE/WRITE_SIZE measurement (profiles/decode_traffic.json) when
-present. ``cpu_baseline`` times the oracle's dequantize-then-matmul (numpy, all
-host cores) on config 1.
+present. ``cpu_baseline`` times the oracle's dequantize-then-matmul (its C dequant with
+OpenMP, then a numpy float32 BLAS matmul, on the box's CPU share) on config 1.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
        [--only decode|prefill|fp8|moe|copy|crossover [--m 1,2,...]] [--eager] [--no-cpu]
@@ -72,15 +72,18 @@ def parse():
 
 
 def cpu_baseline(budget_s=15.0):
-    """Oracle dequantize-then-matmul on the host cores, config 1 (M=16, K=N=4096)."""
+    """Oracle dequantize-then-matmul on the host cores, config 1 (M=16, K=N=4096): the C
+    restatement of the dequant (OpenMP) and a float32 BLAS matmul, both on `threads` threads
+    (the box's CPU share, OMP_NUM_THREADS, else the cores this process may run on)."""
     from oracle import oracle as O
-    cores = len(os.sched_getaffinity(0))
+    from oracle import oracle_c as C
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
     x, packed, scale = O.make_w4a16(16, 4096, 4096, GROUP, seed=1)
     times, tdq, tmm = [], [], []
     t_end = time.perf_counter() + budget_s
     while True:
         t0 = time.perf_counter()
-        w = O.dequant_int4(packed, scale, 1, GROUP)
+        w = C.dequant_int4(packed, scale, 1, GROUP, threads=threads)
         t1 = time.perf_counter()
         y = x @ w.T  # float32 BLAS, fp32 accumulation (test_marlin.cpp:108-111)
         O.bf16_round(y)
@@ -94,11 +97,11 @@ def cpu_baseline(budget_s=15.0):
     return {
         "value": round(w4a16_bytes(16, 4096, 4096) / med / 1e9, 4),
         "unit": "GB/s",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
         "sample": f"config 1 (M=16, K=N=4096, int4 g128) x{len(times)} runs, median "
-                  f"{med * 1e3:.1f} ms (dequant {np.median(tdq) * 1e3:.1f} ms, matmul {np.median(tmm) * 1e3:.1f} ms), "
-                  f"numpy oracle, BLAS threads = host cores",
+                  f"{med * 1e3:.2f} ms (dequant {np.median(tdq) * 1e3:.2f} ms: the oracle's C restatement, "
+                  f"OpenMP; matmul {np.median(tmm) * 1e3:.2f} ms: numpy float32 BLAS), {threads} threads",
     }
 
 

@@ -5,6 +5,9 @@ TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the
 checker (or, in the bench, as the timed CPU baseline). The product path
 (``pulsarlm_amd``) never imports it and has no CPU fallback.
 
+(``oracle/dequant.c``, loaded by ``oracle/oracle_c.py``, restates the int4 dequant once
+more in C with OpenMP for the host baseline; tests check it against this module bit for bit.)
+
 It restates, in numpy, the arithmetic of the reference's Marlin dequant-GEMM
 path in pulsarlm-core:
 
