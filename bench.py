@@ -292,14 +292,13 @@ def section_moe(b: Bench):
 
 
 def section_crossover(b: Bench, ms):
-    """The decode kernel against the MFMA kernel around M = 16 (o and gate_up, int4 g128):
-    run once as is and once with PLM_DECODE_MAX_M=0 (every M on the MFMA kernel)."""
+    """The decode kernel against the MFMA kernel around M = 16 (the Qwen3-8B layers, int4
+    g128): run with PLM_DECODE_MAX_M=0 (every M on the MFMA kernel) and with it at 16 or 32."""
     torch, L = b.torch, b._lib
-    limit = int(os.environ.get("PLM_DECODE_MAX_M", "16"))
-    out = {"decode_max_m": limit}
+    env = os.environ.get("PLM_DECODE_MAX_M")
+    limit = int(env) if env is not None else None  # None: the library's own rule
+    out = {"decode_max_m": limit if limit is not None else "rule"}
     for i, (name, k, n) in enumerate(SHAPES):
-        if name not in ("o", "gate_up"):
-            continue
         copies = b.int4_layer(k, n, i, min_copies=2)
         for m in ms:
             x = torch.randn(m, k, device=b.dev).to(torch.bfloat16)
@@ -308,7 +307,8 @@ def section_crossover(b: Bench, ms):
             tt = b.time(launches, reps=5) / len(copies)
             gbs = w4a16_bytes(m, n, k) / tt / 1e9
             tf = 2 * m * n * k / tt / 1e12
-            out[f"{name}_m{m}"] = {"kernel": "decode" if m <= min(limit, 16) else "mfma", "us": round(tt * 1e6, 2),
+            kernel = "rule" if limit is None else ("decode" if m <= limit else "mfma")
+            out[f"{name}_m{m}"] = {"kernel": kernel, "us": round(tt * 1e6, 2),
                                    "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3),
                                    "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
         del copies

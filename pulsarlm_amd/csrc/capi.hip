@@ -1,7 +1,7 @@
 // C-ABI GEMM entry points: argument checks (mirroring gemm<fmt>,
 // pulsarlm-core/src/kernels/marlin.cu:538-576) and dispatch between the decode
-// kernel (M <= 16, the reference's small_m switch at marlin.cu:577) and the MFMA
-// kernel.
+// kernels (M <= 16, the reference's small_m switch at marlin.cu:577, and up to 32 rows
+// where measured faster) and the MFMA kernel.
 #include <algorithm>
 #include <cstdlib>
 
@@ -20,16 +20,25 @@ int launch_quantize_rows(const char* op, const void* x, bool bf16, int64_t m, in
 int64_t decode_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k);
 int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k, bool a8);
 
-// Largest M served by the decode kernels (their MFMA tiles hold 16 rows); above it the MFMA
-// kernel runs. Environment PLM_DECODE_MAX_M (0-16) lowers it, for measuring one path
-// against the other at the same M.
-int64_t decode_max_m() {
+// Decode kernels or MFMA kernel. The decode kernels take up to 32 rows (one or two 16-row
+// MFMA blocks; W8A8 one). Measured on MI355X at the Qwen3-8B shapes (both paths at every M
+// from 1 to 64): decode is 1.6-2.9x faster up to 16 rows, and 18-35 % faster from 17 to 32
+// rows except for the widest layer (N = 24576, four or more 16-column strips per CU),
+// where it stops winning above 24 rows. Environment PLM_DECODE_MAX_M (0-32) replaces the
+// rule by a plain threshold, for measuring one path against the other at the same M.
+int64_t decode_env_max_m() {
     static const int64_t v = [] {
         const char* e = getenv("PLM_DECODE_MAX_M");
-        return e == nullptr ? int64_t{16} : std::min<int64_t>(16, std::max<int64_t>(0, atoll(e)));
+        return e == nullptr ? int64_t{-1} : std::min<int64_t>(32, std::max<int64_t>(0, atoll(e)));
     }();
     return v;
 }
+bool use_decode(int64_t m, int64_t n) {
+    if (decode_env_max_m() >= 0) return m <= decode_env_max_m();
+    if (m <= 16) return true;
+    return m <= 32 && (m <= 24 || ceil_div(n, kTileN) < 4 * cu_count());
+}
+bool use_decode_w8a8(int64_t m) { return m <= 16 && (decode_env_max_m() < 0 || m <= decode_env_max_m()); }
 
 const char* gemm_op_name(plm_format f) { return f == PLM_INT4 ? "gemm_int4_marlin" : "gemm_fp8_marlin"; }
 
@@ -63,7 +72,7 @@ extern "C" {
 
 int64_t plm_gemm_workspace_bytes(plm_format format, int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0) return 0;
-    return m <= decode_max_m() ? decode_workspace_bytes(format, m, n, k) : mfma_workspace_bytes(format, m, n, k, false);
+    return use_decode(m, n) ? decode_workspace_bytes(format, m, n, k) : mfma_workspace_bytes(format, m, n, k, false);
 }
 
 int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype, const void* weight, const void* scale,
@@ -75,7 +84,7 @@ int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype, const void* we
         return rc;
     if (m == 0 || n == 0) return PLM_OK;
     const bool bf16 = x_dtype == PLM_BF16;
-    if (m <= decode_max_m())
+    if (use_decode(m, n))
         return launch_decode(op, format, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y,
                              workspace, workspace_bytes, as_stream(stream), nullptr, nullptr);
     return launch_mfma(op, format, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, workspace,
@@ -94,7 +103,8 @@ w8a8_ws w8a8_layout(int64_t m, int64_t n, int64_t k) {
     w8a8_ws w{};
     // The split-K counters always keep the front of the workspace, even when this call
     // does not split, so scratch written here never lands on them.
-    const int64_t gemm = m <= decode_max_m() ? decode_workspace_bytes(PLM_FP8, m, n, k) : mfma_workspace_bytes(PLM_FP8, m, n, k, true);
+    const int64_t gemm = use_decode_w8a8(m) ? decode_workspace_bytes(PLM_FP8, m, n, k)
+                                            : mfma_workspace_bytes(PLM_FP8, m, n, k, true);
     w.gemm = round_up(std::max<int64_t>(gemm, kCounterBytes), 256);
     w.xq = round_up(m * ceil_div(k, kTileK) * kTileK, 256);
     w.sx = round_up(m * 4, 256);
@@ -143,7 +153,7 @@ int plm_gemm_w8a8(const void* x, plm_dtype x_dtype, const void* weight, const vo
     const bool bf16 = x_dtype == PLM_BF16;
     hipStream_t s = as_stream(stream);
     if (int rc = launch_quantize_rows(op, x, bf16, m, k, xq, sx, true, s)) return rc;
-    if (m <= decode_max_m())
+    if (use_decode_w8a8(m))
         return launch_decode(op, PLM_FP8, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, base,
                              static_cast<size_t>(l.gemm), s, xq, sx);
     return launch_mfma(op, PLM_FP8, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, base,

@@ -53,11 +53,12 @@ struct decode_args {
     int xs_row, xs_wave;
 };
 
-// One wavefront's batch of TPW K tiles for SP strips: weights, raw scale bits and x.
-template <plm_format F, int SP, int TPW, bool A8> struct decode_batch {
+// One wavefront's batch of TPW K tiles for SP strips: weights, raw scale bits and x (RB
+// blocks of 16 rows).
+template <plm_format F, int SP, int TPW, bool A8, int RB> struct decode_batch {
     u32x4_t w[TPW][SP][fmt_traits<F>::tile_bytes / 1024];
     uint32_t s[TPW][SP];
-    u32x4_t x[TPW][A8 ? 2 : 4];  // bf16/fp16: 4 steps x 8 values; e4m3: 32 bytes
+    u32x4_t x[TPW][RB][A8 ? 2 : 4];  // bf16/fp16: 4 steps x 8 values; e4m3: 32 bytes
 };
 
 // Loads are raw buffer loads issued unconditionally, so no load sits behind a branch or
@@ -73,8 +74,14 @@ template <plm_format F, int SP, int TPW, bool A8> struct decode_batch {
 // K tile is one v_mfma_scale_f32_16x16x128_f8f6f4 per strip on the raw weight bytes,
 // the tile's partial is multiplied by its fp32 block scale, and the row scale is
 // applied before the reduction.
-template <plm_format F, bool BF16, int SP, int TPW, int NW, bool UNIFORM, bool WIDE, bool A8 = false, bool XS = false>
+//
+// RB = 2 (16 < M <= 32, bf16/fp16 x read from global memory): each dequantized weight
+// fragment feeds two MFMAs, one per 16-row block, so the weights are still read and
+// dequantized once.
+template <plm_format F, bool BF16, int SP, int TPW, int NW, bool UNIFORM, bool WIDE, bool A8 = false, bool XS = false,
+          int RB = 1>
 __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
+    static_assert(RB == 1 || (!A8 && !XS), "two row blocks: bf16/fp16 x read from global memory only");
     constexpr int TB = fmt_traits<F>::tile_bytes;
     constexpr int ES = WIDE ? 4 : 2;  // scale element bytes
     const int lane = threadIdx.x & 63;
@@ -104,12 +111,17 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
         A8 ? make_rsrc(a.xq, static_cast<uint32_t>(a.m) * a.ktiles * kTileK)
            : make_rsrc(a.x, static_cast<uint32_t>(a.m) * a.k * 2);
     // bf16/fp16: row * K * 2 + 16 kq (+ 64 t + 256 kt); e4m3: row * ktiles * 128 + 32 kq (+ 128 kt).
-    const int x_lane = A8 ? (col16 < a.m ? col16 * a.ktiles * kTileK : kOOB) + 32 * kq
-                          : (col16 < a.m ? col16 * a.k * 2 : kOOB) + 16 * kq;
+    int x_lane[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int row = 16 * rb + col16;
+        x_lane[rb] = A8 ? (row < a.m ? row * a.ktiles * kTileK : kOOB) + 32 * kq
+                        : (row < a.m ? row * a.k * 2 : kOOB) + 16 * kq;
+    }
     const int w_lane = lane * 16;
     const int s_lane = (a.scale_cols == 1 ? 0 : col16) * ES;
 
-    auto load_batch = [&](decode_batch<F, SP, TPW, A8>& b, int kt0) {
+    auto load_batch = [&](decode_batch<F, SP, TPW, A8, RB>& b, int kt0) {
 #pragma unroll
         for (int tt = 0; tt < TPW; ++tt) {
             const int kt = kt0 + tt;
@@ -127,18 +139,22 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
                 }
             }
             if constexpr (A8) {
-                b.x[tt][0] = buffer_load16(xr, x_lane, x_off);
-                b.x[tt][1] = buffer_load16(xr, x_lane + 16, x_off);
+                b.x[tt][0][0] = buffer_load16(xr, x_lane[0], x_off);
+                b.x[tt][0][1] = buffer_load16(xr, x_lane[0] + 16, x_off);
             } else if constexpr (!XS) {
 #pragma unroll
-                for (int t = 0; t < 4; ++t) b.x[tt][t] = buffer_load16(xr, x_lane + 64 * t, x_off);
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) b.x[tt][rb][t] = buffer_load16(xr, x_lane[rb] + 64 * t, x_off);
             }
         }
     };
 
-    f32x4_t acc[SP];
+    f32x4_t acc[RB][SP];
 #pragma unroll
-    for (int j = 0; j < SP; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int j = 0; j < SP; ++j) acc[rb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     // XS: the wavefront copies its K range of x (rows < M, xs_row bytes each) into its own
     // LDS area with buffer loads to LDS, 1 KiB per instruction, instead of issuing four
@@ -156,7 +172,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
         }
     }
 
-    auto compute_batch = [&](const decode_batch<F, SP, TPW, A8>& b, int kt0) {
+    auto compute_batch = [&](const decode_batch<F, SP, TPW, A8, RB>& b, int kt0) {
 #pragma unroll
         for (int tt = 0; tt < TPW; ++tt) {
             const int kt = kt0 + tt;
@@ -165,27 +181,31 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
 #pragma unroll
                 for (int j = 0; j < SP; ++j) {
                     const float s = scale_from_bits<WIDE>(b.s[tt][j], bf16_scale);
-                    const i32x8_t av = __builtin_bit_cast(i32x8_t, u32x8_cat(b.x[tt][0], b.x[tt][1]));
+                    const i32x8_t av = __builtin_bit_cast(i32x8_t, u32x8_cat(b.x[tt][0][0], b.x[tt][0][1]));
                     const i32x8_t bv = __builtin_bit_cast(i32x8_t, u32x8_cat(b.w[tt][j][0], b.w[tt][j][TB / 1024 - 1]));
                     const f32x4_t part = mfma16x16x128_fp8(av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[j][i] = __builtin_fmaf(s, part[i], acc[j][i]);
+                    for (int i = 0; i < 4; ++i) acc[0][j][i] = __builtin_fmaf(s, part[i], acc[0][j][i]);
                 }
                 continue;
             }
-            u32x4_t xs[4];
+            u32x4_t xs[RB][4];
             if constexpr (XS) {
                 const uint8_t* xr_lds = xs_wave + min(col16, a.m - 1) * a.xs_row + (kt - w_lo) * 256 + kq * 16;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) xs[t] = *reinterpret_cast<const u32x4_t*>(xr_lds + 64 * t);
+                for (int t = 0; t < 4; ++t) xs[0][t] = *reinterpret_cast<const u32x4_t*>(xr_lds + 64 * t);
             } else {
 #pragma unroll
-                for (int t = 0; t < 4; ++t) xs[t] = b.x[tt][t];
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) xs[rb][t] = b.x[tt][rb][t];
             }
             if ((kt + 1) * kTileK > a.k) {  // wave-uniform: partial last tile, zero x past K
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    if (kt * kTileK + 32 * t + 8 * kq >= a.k) xs[t] = u32x4_t{0u, 0u, 0u, 0u};
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        if (kt * kTileK + 32 * t + 8 * kq >= a.k) xs[rb][t] = u32x4_t{0u, 0u, 0u, 0u};
             }
 #pragma unroll
             for (int j = 0; j < SP; ++j) {
@@ -214,7 +234,8 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
                         const u32x4_t& v = b.w[tt][j][t >> 1];
                         bop = dq_fp8<BF16>(v[(t & 1) * 2], v[(t & 1) * 2 + 1], s);
                     }
-                    acc[j] = mfma16x16x32<BF16>(xs[t], bop, acc[j]);
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) acc[rb][j] = mfma16x16x32<BF16>(xs[rb][t], bop, acc[rb][j]);
                 }
             }
         }
@@ -222,7 +243,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
 
     // One batch in flight per wavefront; latency is hidden by the other resident
     // wavefronts (a register double buffer gets rotated into copies that wait).
-    decode_batch<F, SP, TPW, A8> b;
+    decode_batch<F, SP, TPW, A8, RB> b;
     for (int kt = w_lo; kt < w_hi; kt += TPW) {
         load_batch(b, kt);
         if constexpr (XS) {
@@ -239,20 +260,22 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
         for (int i = 0; i < 4; ++i) {
             const float sx = a.x_scale[min(4 * kq + i, a.m - 1)];
 #pragma unroll
-            for (int j = 0; j < SP; ++j) acc[j][i] *= sx;
+            for (int j = 0; j < SP; ++j) acc[0][j][i] *= sx;
         }
     }
 
-    // Cross-wavefront reduction in a fixed order.
-    __shared__ float red[NW][SP][64][4];
+    // Cross-wavefront reduction in a fixed order; slot rb * SP + j holds row block rb, strip j.
+    __shared__ float red[NW][RB * SP][64][4];
     __shared__ uint32_t last_flag;
 #pragma unroll
-    for (int j = 0; j < SP; ++j)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave][j][lane][i] = acc[j][i];
+        for (int j = 0; j < SP; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave][rb * SP + j][lane][i] = acc[rb][j][i];
     __syncthreads();
 
-    constexpr int kElems = SP * 64 * 4;
+    constexpr int kElems = RB * SP * 64 * 4;
     constexpr int kPer = (kElems + NW * 64 - 1) / (NW * 64);
     float sum[kPer];
     int rows[kPer];
@@ -262,12 +285,12 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
         const int e = threadIdx.x + r * NW * 64;
         rows[r] = -1;
         if (e < kElems) {
-            const int i = e & 3, ln = (e >> 2) & 63, j = e >> 8;
+            const int i = e & 3, ln = (e >> 2) & 63, slot = e >> 8, j = slot % SP, rb = slot / SP;
             float v = 0.f;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) v += red[w][j][ln][i];
+            for (int w = 0; w < NW; ++w) v += red[w][slot][ln][i];
             sum[r] = v;
-            const int row = 4 * (ln >> 4) + i;
+            const int row = 16 * rb + 4 * (ln >> 4) + i;
             const int col = (sg * SP + j) * kTileN + (ln & 15);
             if (row < a.m && col < a.n) {
                 rows[r] = row;
@@ -571,10 +594,20 @@ int64_t decode_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k) {
 }
 
 namespace {
-template <plm_format F, bool BF16, int SP, int TPW, int NW>
+template <plm_format F, bool BF16, int SP, int TPW, int NW, int RB = 1>
 void launch_decode_t(const decode_args& a, int strip_groups, bool uniform, hipStream_t s) {
     dim3 grid(strip_groups, a.splits);
     const bool wide = a.scale_dtype == PLM_FP32;
+    if constexpr (RB == 2) {  // 16 < M <= 32: x from global memory, no W8A8
+        if (uniform) {
+            if (wide) decode_kernel<F, BF16, SP, TPW, NW, true, true, false, false, 2><<<grid, NW * 64, 0, s>>>(a);
+            else decode_kernel<F, BF16, SP, TPW, NW, true, false, false, false, 2><<<grid, NW * 64, 0, s>>>(a);
+        } else {
+            if (wide) decode_kernel<F, BF16, SP, TPW, NW, false, true, false, false, 2><<<grid, NW * 64, 0, s>>>(a);
+            else decode_kernel<F, BF16, SP, TPW, NW, false, false, false, false, 2><<<grid, NW * 64, 0, s>>>(a);
+        }
+        return;
+    }
     if constexpr (F == PLM_FP8) {
         if (a.xq != nullptr) {  // W8A8 (group_size % 128 == 0 is checked by the caller)
             if (wide) decode_kernel<F, BF16, SP, TPW, NW, true, true, true><<<grid, NW * 64, 0, s>>>(a);
@@ -602,26 +635,26 @@ void launch_decode_t(const decode_args& a, int strip_groups, bool uniform, hipSt
     }
 }
 
-template <plm_format F, bool BF16, int SP, int TPW>
+template <plm_format F, bool BF16, int SP, int TPW, int RB>
 void launch_decode_nw(const decode_args& a, const decode_config& c, bool uniform, hipStream_t s) {
     switch (c.nw) {
-        case 4: launch_decode_t<F, BF16, SP, TPW, 4>(a, c.strip_groups, uniform, s); break;
-        case 8: launch_decode_t<F, BF16, SP, TPW, 8>(a, c.strip_groups, uniform, s); break;
-        default: launch_decode_t<F, BF16, SP, TPW, 16>(a, c.strip_groups, uniform, s); break;
+        case 4: launch_decode_t<F, BF16, SP, TPW, 4, RB>(a, c.strip_groups, uniform, s); break;
+        case 8: launch_decode_t<F, BF16, SP, TPW, 8, RB>(a, c.strip_groups, uniform, s); break;
+        default: launch_decode_t<F, BF16, SP, TPW, 16, RB>(a, c.strip_groups, uniform, s); break;
     }
 }
 
-template <plm_format F, bool BF16, int SP>
+template <plm_format F, bool BF16, int SP, int RB>
 void launch_decode_sp(const decode_args& a, const decode_config& c, bool uniform, hipStream_t s) {
-    if (c.tpw == 1) launch_decode_nw<F, BF16, SP, 1>(a, c, uniform, s);
-    else launch_decode_nw<F, BF16, SP, 2>(a, c, uniform, s);
+    if (c.tpw == 1) launch_decode_nw<F, BF16, SP, 1, RB>(a, c, uniform, s);
+    else launch_decode_nw<F, BF16, SP, 2, RB>(a, c, uniform, s);
 }
 
-template <plm_format F, bool BF16>
+template <plm_format F, bool BF16, int RB = 1>
 void launch_decode_f(const decode_args& a, const decode_config& c, bool uniform, hipStream_t s) {
-    if (c.sp == 1) launch_decode_sp<F, BF16, 1>(a, c, uniform, s);
-    else if (c.sp == 2) launch_decode_sp<F, BF16, 2>(a, c, uniform, s);
-    else launch_decode_t<F, BF16, 4, 1, 16>(a, c.strip_groups, uniform, s);
+    if (c.sp == 1) launch_decode_sp<F, BF16, 1, RB>(a, c, uniform, s);
+    else if (c.sp == 2) launch_decode_sp<F, BF16, 2, RB>(a, c, uniform, s);
+    else launch_decode_t<F, BF16, 4, 1, 16, RB>(a, c.strip_groups, uniform, s);
 }
 }  // namespace
 
@@ -805,6 +838,18 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
                 return PLM_OK;
             }
         }
+    }
+    if (m > 16) {  // two 16-row blocks per MFMA pass (the caller sends W8A8 only up to 16 rows)
+        PLM_CHECK_ARG(m <= 32 && xq == nullptr, op, "the decode kernels take at most 32 rows (16 for W8A8)");
+        if (f == PLM_INT4) {
+            if (bf16) launch_decode_f<PLM_INT4, true, 2>(a, c, uniform, s);
+            else launch_decode_f<PLM_INT4, false, 2>(a, c, uniform, s);
+        } else {
+            if (bf16) launch_decode_f<PLM_FP8, true, 2>(a, c, uniform, s);
+            else launch_decode_f<PLM_FP8, false, 2>(a, c, uniform, s);
+        }
+        PLM_HIP_LAUNCH_CHECK(op);
+        return PLM_OK;
     }
     if (f == PLM_INT4) {
         if (bf16) launch_decode_f<PLM_INT4, true>(a, c, uniform, s);

@@ -67,7 +67,7 @@ def test_config4_qwen3_27b_shapes(shape, m):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
-@pytest.mark.parametrize("m", [1, 4, 16, 17, 100, 300])
+@pytest.mark.parametrize("m", [1, 4, 16, 17, 25, 32, 100, 300])
 def test_w8a16_32x32_blocks(m, dtype):
     """The reference's model-level fp8 configuration (test_qwen3_5.cpp:691-696): 32 x 32
     quantization blocks, so block_n = 32 (one scale per two 16-column strips) and 32-wide

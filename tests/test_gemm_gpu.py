@@ -279,14 +279,50 @@ def test_full_size_against_gpu_fp32(shape, m):
 
 
 def test_decode_and_mfma_kernels_agree():
-    """M=16 runs the decode kernel and M=17 the MFMA kernel; their first 16 rows must agree
-    to the GEMM tolerance (both are checked against the oracle elsewhere)."""
+    """M=16 and M=32 run the decode kernels (one and two 16-row blocks), M=33 the MFMA
+    kernel; their common rows must agree to the GEMM tolerance (each is checked against the
+    oracle elsewhere)."""
     k, n = 12288, 4096
-    x, packed, s = _full_case(17, k, n, seed=5)
+    x, packed, s = _full_case(33, k, n, seed=5)
     w, sc = ops.repack_int4_marlin_cuda(packed, s, 1, 128)
     a = ops.gemm_int4_marlin_cuda(x[:16].contiguous(), w, sc, n, 1, 128)
-    b = ops.gemm_int4_marlin_cuda(x, w, sc, n, 1, 128)[:16]
-    assert torch.allclose(a.float(), b.float(), atol=2e-2, rtol=2e-2)
+    b = ops.gemm_int4_marlin_cuda(x[:32].contiguous(), w, sc, n, 1, 128)
+    c = ops.gemm_int4_marlin_cuda(x, w, sc, n, 1, 128)
+    assert torch.allclose(a.float(), c[:16].float(), atol=2e-2, rtol=2e-2)
+    assert torch.allclose(b.float(), c[:32].float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("m", [17, 20, 24, 28, 31, 32])
+@pytest.mark.parametrize("shape", [(4096, 6144), (4096, 4096), (4096, 24576), (12288, 4096)])
+def test_two_row_block_decode(shape, m):
+    """17 to 32 rows: the decode kernels with two 16-row MFMA blocks per dequantized weight
+    fragment (gate_up above 24 rows goes to the MFMA kernel), rows past M of the second
+    block never stored."""
+    k, n = shape
+    x, packed, s = O.make_w4a16(m, n, k, 128, seed=k + n + m)
+    w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), to_dev(s), 1, 128)
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, torch.bfloat16), w, sc, n, 1, 128)
+    assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, 128), None), f"{shape} m={m}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("case", ["fp16s", "fp32s-strip", "g256", "g64"])
+def test_two_row_block_decode_variants(case, dtype):
+    """Two row blocks across scale layouts, groups below and above one K tile, fp16 x and a
+    ragged strip count (N = 8200)."""
+    m, n, k, g, block_n, sdt = 23, 8200, 512, 128, 1, np.float16
+    if case == "fp32s-strip":
+        block_n, sdt = 128, np.float32
+    elif case == "g256":
+        g = 256
+    elif case == "g64":
+        g = 64
+    packed, s = int4_case(n, k, g, block_n, seed=len(case))
+    s = s.astype(sdt)
+    w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), scale_tensor(s), block_n, g)
+    x = x_case(m, k, dtype, seed=m)
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, TDT[dtype]), w, sc, n, block_n, g)
+    assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, block_n, g, dtype), None), f"{case} {dtype}")
 
 
 @pytest.mark.parametrize("m", [1, 4, 7, 16])
