@@ -112,7 +112,8 @@ int64_t plm_gemm_workspace_bytes(plm_format format, int64_t m, int64_t n, int64_
  * y [M, N] = x [M, K] @ dequant(W)^T, x and y in x_dtype (PLM_BF16 or PLM_FP16),
  * fp32 accumulation. Replaces gemm_int4_marlin_cuda / gemm_fp8_marlin_cuda
  * (ops.hpp:327-343, marlin.cu:538-597,631-651).
- * M <= 16 runs the bandwidth-first decode kernel; larger M the MFMA kernel.
+ * M <= 16 (and up to 32 rows where measured faster) runs the bandwidth-first decode kernels;
+ * larger M the MFMA kernel.
  * M == 0 or N == 0 returns PLM_OK without touching y.
  */
 int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype,

@@ -1,4 +1,5 @@
-// Bandwidth-first dequant-GEMM for decode (M <= 16): y[M, N] = x[M, K] @ dequant(W)^T.
+// Bandwidth-first dequant-GEMM for decode (M <= 16, and 17-32 rows as two 16-row blocks):
+// y[M, N] = x[M, K] @ dequant(W)^T.
 //
 // Counterpart of the reference's marlin_kernel at tile_m = 16 (pulsarlm-core/src/kernels/
 // marlin.cu:251-389, dispatched for M <= 16 at :577-596) together with its split-K
