@@ -131,6 +131,59 @@ def test_linear_quantized_matches_dense(kind):
     assert torch.allclose(y.float(), ref.float(), 2e-2, 2e-2)
 
 
+def _quantize_int4(w, group):
+    """Symmetric int4 per (row, group): scale = amax / 7 stored as fp16, q = clamp(round(w / s))."""
+    n, k = w.shape
+    blocks = w.float().view(n, k // group, group)
+    scale = (blocks.abs().amax(-1) / 7).clamp_min(1e-8).to(torch.float16)
+    q = torch.clamp(torch.round(blocks / scale.float()[..., None]), -8, 7).to(torch.int32).view(n, k)
+    nib = q.bitwise_and(0xF).to(torch.long).view(n, k // 8, 8)
+    packed = nib.bitwise_left_shift(torch.arange(0, 32, 4, device=w.device)).sum(-1).to(torch.int32)
+    dense = q.to(torch.bfloat16) * scale.repeat_interleave(group, 1).to(torch.bfloat16)
+    return packed, scale, dense
+
+
+def _quantize_fp8(w, block):
+    """The test_qwen3_5.cpp:301-311 block quantizer: scale = max(amax, 1e-12) / 448 per
+    block x block tile, codes = e4m3(w / scale)."""
+    n, k = w.shape
+    t = w.float().view(n // block, block, k // block, block)
+    scale = (t.abs().amax(dim=(1, 3)).clamp_min(1e-12) / 448).contiguous()
+    codes = (t / scale[:, None, :, None]).view(n, k).to(torch.float8_e4m3fn)
+    full = scale.repeat_interleave(block, 0).repeat_interleave(block, 1)
+    dense = codes.to(torch.bfloat16) * full.to(torch.bfloat16)
+    return codes, scale, dense
+
+
+@pytest.mark.parametrize("kind", ["int4", "fp8_32", "fp8_128"])
+@pytest.mark.parametrize("m", [1, 16, 24, 64])
+def test_mlp_block_quantized_matches_dense(kind, m):
+    """A Qwen3-style MLP block (gate_up, silu·mul, down) through linear::int4 / linear::fp8
+    and silu_mul_cuda, against the same block on the dequantized weights in fp32: the
+    model-level comparison of test_qwen3_5.cpp:691-696 (fp8 in 32 x 32 blocks there), with its
+    bound, max |y - ref| / max |ref| < 5e-2. M = 1 and 16 run the decode kernels, 24 the
+    two-row-block decode kernels, 64 the MFMA kernel."""
+    hidden, inter = 512, 1024
+    g = gen(40 + m)
+    w_gu = (torch.randn((2 * inter, hidden), generator=g, **cuda(torch.float)) * 0.02).to(torch.bfloat16)
+    w_dn = (torch.randn((hidden, inter), generator=g, **cuda(torch.float)) * 0.02).to(torch.bfloat16)
+    x = torch.randn((m, hidden), generator=g, **cuda(torch.bfloat16))
+    if kind == "int4":
+        p_gu, s_gu, d_gu = _quantize_int4(w_gu, 128)
+        p_dn, s_dn, d_dn = _quantize_int4(w_dn, 128)
+        lin_gu, lin_dn = _host.linear.int4(p_gu, s_gu, 1, 128), _host.linear.int4(p_dn, s_dn, 1, 128)
+    else:
+        b = 32 if kind == "fp8_32" else 128
+        c_gu, s_gu, d_gu = _quantize_fp8(w_gu, b)
+        c_dn, s_dn, d_dn = _quantize_fp8(w_dn, b)
+        lin_gu, lin_dn = _host.linear.fp8(c_gu, s_gu, b, b), _host.linear.fp8(c_dn, s_dn, b, b)
+    y = lin_dn.apply(_host.silu_mul_cuda(lin_gu.apply(x)))
+    h = x.float() @ d_gu.float().T
+    ref = (torch.nn.functional.silu(h[:, :inter]) * h[:, inter:]) @ d_dn.float().T
+    err = ((y.float() - ref).abs().max() / ref.abs().max()).item()
+    assert err < 5e-2, f"{kind} m={m}: max relative error {err:.3g}"
+
+
 # ------------------------------------------------- router and activation (test_fused_ops.cpp)
 
 
