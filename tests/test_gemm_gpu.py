@@ -306,10 +306,10 @@ def test_two_row_block_decode(shape, m):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
-@pytest.mark.parametrize("case", ["fp16s", "fp32s-strip", "g256", "g64"])
+@pytest.mark.parametrize("case", ["fp16s", "fp32s-strip", "g256", "g64", "k-tail"])
 def test_two_row_block_decode_variants(case, dtype):
-    """Two row blocks across scale layouts, groups below and above one K tile, fp16 x and a
-    ragged strip count (N = 8200)."""
+    """Two row blocks across scale layouts, groups below and above one K tile, fp16 x, a
+    ragged strip count (N = 8200) and a partial last K tile (K = 400, 16-wide groups)."""
     m, n, k, g, block_n, sdt = 23, 8200, 512, 128, 1, np.float16
     if case == "fp32s-strip":
         block_n, sdt = 128, np.float32
@@ -317,6 +317,8 @@ def test_two_row_block_decode_variants(case, dtype):
         g = 256
     elif case == "g64":
         g = 64
+    elif case == "k-tail":
+        m, n, k, g = 29, 300, 400, 16
     packed, s = int4_case(n, k, g, block_n, seed=len(case))
     s = s.astype(sdt)
     w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), scale_tensor(s), block_n, g)
