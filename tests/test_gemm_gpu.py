@@ -327,7 +327,7 @@ def test_two_row_block_decode_variants(case, dtype):
     assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, block_n, g, dtype), None), f"{case} {dtype}")
 
 
-@pytest.mark.parametrize("m", [1, 4, 7, 16])
+@pytest.mark.parametrize("m", [1, 4, 7, 16, 17, 32])
 @pytest.mark.parametrize("n,k,g", [(16, 128, 128), (48, 128, 128), (40, 256, 256), (1000, 384, 128)])
 def test_decode_small_k_and_narrow_n(m, n, k, g):
     """Decode kernels where most wavefronts of a workgroup own no K tile (K of 1-3 tiles),
