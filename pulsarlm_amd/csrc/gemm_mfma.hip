@@ -374,10 +374,12 @@ struct shape {
     constexpr int bm() const { return wm * mt * 16; }
     constexpr int bs() const { return wn * ns; }
 };
-constexpr shape kHuge{2, 4, 8, 4};   // 256 x 256, 8 wavefronts (int4 only: two stages fill the 160 KiB LDS)
+// The 256-row shapes take int4 weights or W8A8 (fp8 weight tiles staged in LDS beside bf16 x
+// would not fit); kTall also takes fp8 W8A16, whose weight tiles then go to registers.
+constexpr shape kHuge{2, 4, 8, 4};   // 256 x 256, 8 wavefronts (two stages fill the 160 KiB LDS)
                                      // (grouped calls; plain calls use kTall, measured 3 % faster)
-constexpr shape kWide{2, 4, 8, 3};   // 256 x 192, 8 wavefronts (int4 only; N = 6144 gives whole rounds)
-constexpr shape kTall{1, 8, 16, 2};  // 256 x 256, 8 wavefronts of 256 x 32 (int4 only): each strip dequantized once
+constexpr shape kWide{2, 4, 8, 3};   // 256 x 192, 8 wavefronts (N = 6144 gives whole rounds)
+constexpr shape kTall{1, 8, 16, 2};  // 256 x 256, 8 wavefronts of 256 x 32: each strip dequantized once
 constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts
 constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
 // Grouped calls also use short row blocks for experts with few rows.
