@@ -382,15 +382,16 @@ constexpr shape kWide{2, 4, 8, 3};   // 256 x 192, 8 wavefronts (N = 6144 gives 
 constexpr shape kTall{1, 8, 16, 2};  // 256 x 256, 8 wavefronts of 256 x 32: each strip dequantized once
 constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts
 constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
+constexpr shape kSmall8{2, 4, 4, 2};  // 128 x 128, 8 wavefronts of 64 x 32 (int4): 2-12 % over kSmall
 // Grouped calls also use short row blocks for experts with few rows.
 constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
 constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
 constexpr shape kGroupedShapes[5] = {kRows16, kRows64, kSmall, kLarge, kHuge};
 constexpr shape shape_of(int id) {
-    return id == 6 ? kTall : id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
+    return id == 7 ? kSmall8 : id == 6 ? kTall : id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
 }
 // Relative MFMA throughput per unit of tile area, measured on MI355X at the Qwen3-8B shapes.
-constexpr double kShapeRate[7] = {0.75, 0.7, 1.0, 0.65, 0.3, 0.95, 1.03};
+constexpr double kShapeRate[8] = {0.75, 0.7, 1.0, 0.65, 0.3, 0.95, 1.03, 0.8};
 
 }  // namespace
 
@@ -417,6 +418,7 @@ bool no_tail() {
 mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) {
     const bool wide_ok = f == PLM_INT4 || a8;
     const bool tall_ok = wide_ok || f == PLM_FP8;  // fp8 W8A16 runs the tall shape with weights in registers
+    const bool small8_ok = f == PLM_INT4 && !a8;
     const int64_t cus = cu_count();
     const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
     auto config = [&](int id) {
@@ -463,12 +465,12 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
         return static_cast<double>(rounds) * (c.tiles_per_split + 3 + reduce) * area;
     };
     if (const char* env = getenv("PLM_MFMA")) {  // tuning sweeps: S, L, H or R
-        const int id = env[0] == 'X' ? 6 : env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
-        return config(((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok) ? 1 : id);
+        const int id = env[0] == 'E' ? 7 : env[0] == 'X' ? 6 : env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
+        return config(((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok) || (id == 7 && !small8_ok) ? 1 : id);
     }
     mfma_config best = config(0);
-    for (int id : {1, 2, 3, 5, 6}) {
-        if (((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok)) continue;
+    for (int id : {1, 2, 3, 5, 6, 7}) {
+        if (((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok) || (id == 7 && !small8_ok)) continue;
         const mfma_config c = config(id);
         if (cost(c) < cost(best)) best = c;
     }
@@ -503,6 +505,11 @@ void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
         if (shape == 5) {
             mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kWide.wm, kWide.wn, kWide.mt, kWide.ns>
                 <<<grid, kWide.wm * kWide.wn * 64, 0, s>>>(a);
+            return;
+        }
+        if (shape == 7) {
+            mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kSmall8.wm, kSmall8.wn, kSmall8.mt, kSmall8.ns>
+                <<<grid, kSmall8.wm * kSmall8.wn * 64, 0, s>>>(a);
             return;
         }
         if (shape == 6) {
