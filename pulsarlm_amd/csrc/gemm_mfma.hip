@@ -386,12 +386,13 @@ constexpr shape kSmall8{2, 4, 4, 2};  // 128 x 128, 8 wavefronts of 64 x 32 (int
 // Grouped calls also use short row blocks for experts with few rows.
 constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
 constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
+constexpr shape kRows64w8{1, 8, 4, 1};  // 64 x 128, 8 wavefronts of one strip (plain int4 calls)
 constexpr shape kGroupedShapes[5] = {kRows16, kRows64, kSmall, kLarge, kHuge};
 constexpr shape shape_of(int id) {
-    return id == 7 ? kSmall8 : id == 6 ? kTall : id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
+    return id == 8 ? kRows64w8 : id == 7 ? kSmall8 : id == 6 ? kTall : id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
 }
 // Relative MFMA throughput per unit of tile area, measured on MI355X at the Qwen3-8B shapes.
-constexpr double kShapeRate[8] = {0.75, 0.7, 1.0, 0.65, 0.3, 0.95, 1.03, 0.8};
+constexpr double kShapeRate[9] = {0.75, 0.7, 1.0, 0.65, 0.3, 0.95, 1.03, 0.8, 0.7};
 
 }  // namespace
 
@@ -465,12 +466,12 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
         return static_cast<double>(rounds) * (c.tiles_per_split + 3 + reduce) * area;
     };
     if (const char* env = getenv("PLM_MFMA")) {  // tuning sweeps: S, L, H or R
-        const int id = env[0] == 'E' ? 7 : env[0] == 'X' ? 6 : env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
-        return config(((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok) || (id == 7 && !small8_ok) ? 1 : id);
+        const int id = env[0] == 'Q' ? 8 : env[0] == 'E' ? 7 : env[0] == 'X' ? 6 : env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
+        return config(((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok) || (id >= 7 && !small8_ok) ? 1 : id);
     }
     mfma_config best = config(0);
-    for (int id : {1, 2, 3, 5, 6, 7}) {
-        if (((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok) || (id == 7 && !small8_ok)) continue;
+    for (int id : {1, 2, 3, 5, 6, 7, 8}) {
+        if (((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok) || (id >= 7 && !small8_ok)) continue;
         const mfma_config c = config(id);
         if (cost(c) < cost(best)) best = c;
     }
@@ -510,6 +511,11 @@ void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
         if (shape == 7) {
             mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kSmall8.wm, kSmall8.wn, kSmall8.mt, kSmall8.ns>
                 <<<grid, kSmall8.wm * kSmall8.wn * 64, 0, s>>>(a);
+            return;
+        }
+        if (shape == 8) {
+            mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kRows64w8.wm, kRows64w8.wn, kRows64w8.mt, kRows64w8.ns>
+                <<<grid, kRows64w8.wm * kRows64w8.wn * 64, 0, s>>>(a);
             return;
         }
         if (shape == 6) {
