@@ -455,10 +455,38 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
             constexpr int kLoads = CH * SG * NL;
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");
         }
+        // int4: every tile's x fragments and scale constants of this batch are read and set
+        // up before the first dequant, i.e. while the weight loads are still in flight.
+        [[maybe_unused]] u32x4_t xfb[CH][4];
+        [[maybe_unused]] int4_scale k4b[CH][SG];
+        if constexpr (F == PLM_INT4 && !A8) {
+#pragma unroll
+            for (int ii = 0; ii < CH; ++ii) {
+                const int i = min(i0 + ii, slots - 1);
+                const uint8_t* xp = xs + (((xrow << a.nkt_shift) + i) << 8) + kq * 16;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xfb[ii][t] = *reinterpret_cast<const u32x4_t*>(xp + 64 * t);
+#pragma unroll
+                for (int sj = 0; sj < SG; ++sj) {
+                    const uint8_t* sp = ss + (((sj << a.nkt_shift) + i) * EB) + (SC == 2 ? 0 : col16 * (WIDE ? 4 : 2));
+                    const uint32_t bits = WIDE ? *reinterpret_cast<const uint32_t*>(sp)
+                                               : static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(sp));
+                    k4b[ii][sj] = make_int4_scale<BF16>(scale_from_bits<WIDE>(bits, bf16_scale));
+                }
+            }
+        }
 #pragma unroll
         for (int ii = 0; ii < CH; ++ii) {
             const int i = i0 + ii;
             if (i >= nkt_w) break;  // wave-uniform
+            if constexpr (F == PLM_INT4 && !A8) {
+#pragma unroll
+                for (int sj = 0; sj < SG; ++sj)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        acc[sj] = mfma16x16x32<BF16>(xfb[ii][t], dq_int4<BF16>(wv[ii][sj][0][t], k4b[ii][sj]), acc[sj]);
+                continue;
+            }
             if constexpr (A8) {
                 const uint8_t* xp = xs + (((xrow << a.nkt_shift) + i) << 7) + kq * 32;
                 const i32x8_t av = __builtin_bit_cast(
