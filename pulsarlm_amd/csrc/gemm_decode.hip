@@ -123,6 +123,20 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
     const int s_lane = (a.scale_cols == 1 ? 0 : col16) * ES;
 
     auto load_batch = [&](decode_batch<F, SP, TPW, A8, RB>& b, int kt0) {
+        // The batch's scales first: they return first, so the scale constants can be set up
+        // while the weight tiles are still arriving.
+        if constexpr (UNIFORM) {
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) {
+                const int kt = kt0 + tt;
+                const int s_off = kt < w_hi ? (kt * kTileK / a.group_size) * a.scale_cols * ES : kOOB;
+#pragma unroll
+                for (int j = 0; j < SP; ++j) {
+                    if constexpr (WIDE) b.s[tt][j] = buffer_load_u32(sr[j], s_lane, s_off);
+                    else b.s[tt][j] = buffer_load_u16(sr[j], s_lane, s_off);
+                }
+            }
+        }
 #pragma unroll
         for (int tt = 0; tt < TPW; ++tt) {
             const int kt = kt0 + tt;
@@ -133,11 +147,6 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
             for (int j = 0; j < SP; ++j) {
 #pragma unroll
                 for (int h = 0; h < TB / 1024; ++h) b.w[tt][j][h] = buffer_load16_stream(wr[j], w_lane + h * 1024, w_off);
-                if constexpr (UNIFORM) {
-                    const int s_off = ok ? (kt * kTileK / a.group_size) * a.scale_cols * ES : kOOB;
-                    if constexpr (WIDE) b.s[tt][j] = buffer_load_u32(sr[j], s_lane, s_off);
-                    else b.s[tt][j] = buffer_load_u16(sr[j], s_lane, s_off);
-                }
             }
             if constexpr (A8) {
                 b.x[tt][0][0] = buffer_load16(xr, x_lane[0], x_off);
@@ -174,6 +183,23 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
     }
 
     auto compute_batch = [&](const decode_batch<F, SP, TPW, A8, RB>& b, int kt0) {
+        // int4 with uniform groups: the batch's scale constants and (staged) x fragments
+        // are set up before its first dequant.
+        [[maybe_unused]] int4_scale k4b[TPW][SP];
+        [[maybe_unused]] u32x4_t xsb[TPW][4];
+        if constexpr (F == PLM_INT4 && UNIFORM && !A8) {
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) {
+#pragma unroll
+                for (int j = 0; j < SP; ++j) k4b[tt][j] = make_int4_scale<BF16>(scale_from_bits<WIDE>(b.s[tt][j], bf16_scale));
+                if constexpr (XS) {
+                    const int kt = min(kt0 + tt, w_hi - 1);
+                    const uint8_t* xr_lds = xs_wave + min(col16, a.m - 1) * a.xs_row + (kt - w_lo) * 256 + kq * 16;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) xsb[tt][t] = *reinterpret_cast<const u32x4_t*>(xr_lds + 64 * t);
+                }
+            }
+        }
 #pragma unroll
         for (int tt = 0; tt < TPW; ++tt) {
             const int kt = kt0 + tt;
@@ -191,7 +217,10 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
                 continue;
             }
             u32x4_t xs[RB][4];
-            if constexpr (XS) {
+            if constexpr (XS && F == PLM_INT4 && UNIFORM) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xs[0][t] = xsb[tt][t];
+            } else if constexpr (XS) {
                 const uint8_t* xr_lds = xs_wave + min(col16, a.m - 1) * a.xs_row + (kt - w_lo) * 256 + kq * 16;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) xs[0][t] = *reinterpret_cast<const u32x4_t*>(xr_lds + 64 * t);
@@ -215,7 +244,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
                 if constexpr (UNIFORM) {
                     const float raw = scale_from_bits<WIDE>(b.s[tt][j], bf16_scale);
                     s_tile = round_to<BF16>(raw);
-                    if constexpr (F == PLM_INT4) k4 = make_int4_scale<BF16>(raw);
+                    if constexpr (F == PLM_INT4 && !A8) k4 = k4b[tt][j];
                 }
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
