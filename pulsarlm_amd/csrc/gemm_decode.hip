@@ -123,9 +123,10 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
     const int s_lane = (a.scale_cols == 1 ? 0 : col16) * ES;
 
     auto load_batch = [&](decode_batch<F, SP, TPW, A8, RB>& b, int kt0) {
-        // The batch's scales first: they return first, so the scale constants can be set up
-        // while the weight tiles are still arriving.
-        if constexpr (UNIFORM) {
+        // int4: the batch's scales first; they return first, so the scale constants can be
+        // set up while the weight tiles are still arriving (fp8 measured no better).
+        constexpr bool kScalesFirst = UNIFORM && F == PLM_INT4 && !A8;
+        if constexpr (kScalesFirst) {
 #pragma unroll
             for (int tt = 0; tt < TPW; ++tt) {
                 const int kt = kt0 + tt;
@@ -147,6 +148,11 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
             for (int j = 0; j < SP; ++j) {
 #pragma unroll
                 for (int h = 0; h < TB / 1024; ++h) b.w[tt][j][h] = buffer_load16_stream(wr[j], w_lane + h * 1024, w_off);
+                if constexpr (UNIFORM && !kScalesFirst) {
+                    const int s_off = ok ? (kt * kTileK / a.group_size) * a.scale_cols * ES : kOOB;
+                    if constexpr (WIDE) b.s[tt][j] = buffer_load_u32(sr[j], s_lane, s_off);
+                    else b.s[tt][j] = buffer_load_u16(sr[j], s_lane, s_off);
+                }
             }
             if constexpr (A8) {
                 b.x[tt][0][0] = buffer_load16(xr, x_lane[0], x_off);
