@@ -192,6 +192,47 @@ def test_deterministic_across_calls():
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("case", [
+    ("int4", 16, 12288, 4096),  # decode kernel with a K split across workgroups
+    ("int4", 256, 4096, 4096),  # MFMA kernel with a K split (fewer tiles than CUs)
+    ("int4", 4096, 4096, 6144),  # MFMA kernel: whole rounds, then the K-split tail launch
+    ("w8a8", 16, 5120, 5120),  # per-token quantizer, then the W8A8 decode kernel
+])
+def test_gemm_graph_replays_match_eager(case):
+    """plm_gemm captured into a graph: the split-K arrival counters are reset by the last
+    workgroup of every call, so each replay (with eager calls between them) must equal the
+    eager result bit for bit."""
+    fmt, m, k, n = case
+    print(f"graph replay case {case}", flush=True)
+    rng = np.random.default_rng(61)
+    xd = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to("cuda").to(torch.bfloat16)
+    if fmt == "int4":
+        packed = rng.integers(-(2**31), 2**31, size=(n, k // 8), dtype=np.int64).astype(np.int32)
+        s = (np.abs(rng.standard_normal((n, k // 128))) * 0.02 + 1e-3).astype(np.float16)
+        w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), to_dev(s), 1, 128)
+        run = lambda: ops.gemm_int4_marlin_cuda(xd, w, sc, n, 1, 128)  # noqa: E731
+    else:
+        codes, s = fp8_case(n, k, 128, 128, seed=62)
+        w, sc = _repack_fp8(codes, s, 128, 128)
+        run = lambda: ops.gemm_fp8_w8a8_cuda(xd, w, sc, n, 128, 128)  # noqa: E731
+    eager = run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        run()  # the stream's workspace is allocated (zeroed) outside the capture
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = run()
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"{case}: replay {i} differs from the eager result"
+        again = run()
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager), f"{case}: eager call after replay {i} differs"
+
+
 # ------------------------------------------------------------------ Marlin-layout ingest, edge cases
 
 
