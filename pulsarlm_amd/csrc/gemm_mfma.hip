@@ -388,7 +388,8 @@ constexpr shape kSmall8{2, 4, 4, 2};  // 128 x 128, 8 wavefronts of 64 x 32 (int
 constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
 constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
 constexpr shape kRows64w8{1, 8, 4, 1};  // 64 x 128, 8 wavefronts of one strip (plain int4 calls)
-constexpr shape kGroupedShapes[5] = {kRows16, kRows64, kSmall, kLarge, kHuge};
+constexpr shape kRows32{1, 4, 2, 2};  // 32 x 128 (grouped)
+constexpr shape kGroupedShapes[6] = {kRows16, kRows64, kSmall, kLarge, kHuge, kRows32};
 constexpr shape shape_of(int id) {
     return id == 9 ? kLarge8 : id == 8 ? kRows64w8 : id == 7 ? kSmall8 : id == 6 ? kTall : id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
 }
@@ -660,6 +661,7 @@ void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t 
         PLM_GROUPED_CASE(1)
         PLM_GROUPED_CASE(2)
         PLM_GROUPED_CASE(3)
+        PLM_GROUPED_CASE(5)
         default:
             mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kHuge.wm, kHuge.wn, kHuge.mt, kHuge.ns>
                 <<<grid, kHuge.wm * kHuge.wn * 64, 0, s>>>(a);
@@ -668,12 +670,29 @@ void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t 
 }
 }  // namespace
 
-int grouped_block_rows(int shape) { return kGroupedShapes[std::min(std::max(shape, 0), 4)].bm(); }
+int grouped_block_rows(int shape) { return kGroupedShapes[std::min(std::max(shape, 0), 5)].bm(); }
 
-// Row block for a grouped call: about the average rows per expert.
+// Row block for a grouped call, from the average rows per expert. At the Zipf-routed
+// T = 256 block (16 rows per expert on average, the heaviest experts near 250) 32-row tiles
+// measured 6 % faster than 16-row ones and 64-row ones 5 % slower: a weight tile is
+// dequantized once per row block, and the dequant bounds these small GEMMs.
+int grouped_rows_env() {  // PLM_MOE_ROWS=16/32/64 forces the tile rows (tuning sweeps)
+    static const int v = [] {
+        const char* e = getenv("PLM_MOE_ROWS");
+        return e == nullptr ? 0 : atoi(e);
+    }();
+    return v;
+}
 int grouped_shape_for(int64_t rows, int64_t n_experts) {
     const int64_t avg = ceil_div(rows, std::max<int64_t>(n_experts, 1));
-    if (avg <= 24) return 0;
+    switch (grouped_rows_env()) {
+        case 16: return 0;
+        case 32: return 5;
+        case 64: return 1;
+        default: break;
+    }
+    if (avg <= 8) return 0;
+    if (avg <= 24) return 5;
     if (avg <= 96) return 1;
     if (avg <= 192) return 2;
     return 3;
@@ -688,7 +707,7 @@ int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const
                   "problem too large");
     mfma_args a{};
     fill_common(a, x, w, scale, scale_dtype, rows, n, k, block_n, group_size, y);
-    const struct shape sh = kGroupedShapes[std::min(std::max(shape, 0), 4)];
+    const struct shape sh = kGroupedShapes[std::min(std::max(shape, 0), 5)];
     a.splits = 1;
     a.tiles_per_split = a.ktiles;
     a.m_blocks = 1;

@@ -68,11 +68,16 @@ def test_grouped_gemm_matches_per_expert_reference(counts):
     assert_close(y, ref, f"grouped {counts}")
 
 
-# The 16-row grouped tiles (few rows per expert) across scale storage, activation dtype and
-# 256-wide groups, with an expert spanning several tiles and a ragged N.
+# The 16-row grouped tiles (at most 8 rows per expert on average) and the 32-row ones (9-24)
+# across scale storage, activation dtype and 256-wide groups, with an expert spanning several
+# tiles and a ragged N.
+SMALL_COUNTS = {16: [30, 0, 3, 1, 0, 0, 20, 2, 17, 0, 0, 19], 32: [70, 0, 3, 1, 0, 0, 20, 2, 33, 0, 0, 64]}
+
+
+@pytest.mark.parametrize("tile_rows", [16, 32])
 @pytest.mark.parametrize("sdt,xdt,g", [("fp32", "bf16", 128), ("bf16", "fp16", 128), ("fp16", "fp16", 256)])
-def test_grouped_small_tiles(sdt, xdt, g):
-    counts = [70, 0, 3, 1, 0, 0, 20, 2, 33, 0, 0, 64]
+def test_grouped_small_tiles(sdt, xdt, g, tile_rows):
+    counts = SMALL_COUNTS[tile_rows]
     e, n, k = len(counts), 200, 1536
     w, s, deq = _experts(e, n, k, g, seed=11, scale_dtype=sdt, x_dtype=xdt)
     rows = sum(counts)
@@ -85,7 +90,7 @@ def test_grouped_small_tiles(sdt, xdt, g):
         if end > start:
             ref[start:end] = O.gemm_ref(x[start:end], deq[i], None)
         start = end
-    assert_close(y, ref, f"grouped 16-row tiles {sdt} {xdt} g={g}")
+    assert_close(y, ref, f"grouped {tile_rows}-row tiles {sdt} {xdt} g={g}")
 
 
 def _moe_case(t, e, hidden, inter, top_k, g, seed):
