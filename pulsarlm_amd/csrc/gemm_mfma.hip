@@ -377,7 +377,6 @@ struct shape {
 // The 256-row shapes take int4 weights or W8A8 (fp8 weight tiles staged in LDS beside bf16 x
 // would not fit); kTall also takes fp8 W8A16, whose weight tiles then go to registers.
 constexpr shape kHuge{2, 4, 8, 4};   // 256 x 256, 8 wavefronts (two stages fill the 160 KiB LDS)
-                                     // (grouped calls; plain calls use kTall, measured 3 % faster)
 constexpr shape kWide{2, 4, 8, 3};   // 256 x 192, 8 wavefronts (N = 6144 gives whole rounds)
 constexpr shape kTall{1, 8, 16, 2};  // 256 x 256, 8 wavefronts of 256 x 32: each strip dequantized once
 constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts
@@ -389,7 +388,7 @@ constexpr shape kRows16{1, 4, 1, 2};  // 16 x 128
 constexpr shape kRows64{1, 4, 4, 2};  // 64 x 128
 constexpr shape kRows64w8{1, 8, 4, 1};  // 64 x 128, 8 wavefronts of one strip (plain int4 calls)
 constexpr shape kRows32{1, 4, 2, 2};  // 32 x 128 (grouped)
-constexpr shape kGroupedShapes[6] = {kRows16, kRows64, kSmall, kLarge, kHuge, kRows32};
+constexpr shape kGroupedShapes[7] = {kRows16, kRows64, kSmall, kLarge, kHuge, kRows32, kTall};
 constexpr shape shape_of(int id) {
     return id == 9 ? kLarge8 : id == 8 ? kRows64w8 : id == 7 ? kSmall8 : id == 6 ? kTall : id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
 }
@@ -646,7 +645,7 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
 
 // Grouped: `tiles` holds max_tiles (expert, first row, rows) records built on the device;
 // rows are in the grouped (sorted) order and `row_index` optionally gathers them from x.
-// shape indexes kGroupedShapes (int4 experts only); 4 (256 x 256) is for full blocks of rows.
+// shape indexes kGroupedShapes (int4 experts only); 6 (256 x 256 tall) is for full blocks of rows.
 namespace {
 template <bool BF16, bool UNIFORM, bool WIDE>
 void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
@@ -662,6 +661,7 @@ void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t 
         PLM_GROUPED_CASE(2)
         PLM_GROUPED_CASE(3)
         PLM_GROUPED_CASE(5)
+        PLM_GROUPED_CASE(6)
         default:
             mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kHuge.wm, kHuge.wn, kHuge.mt, kHuge.ns>
                 <<<grid, kHuge.wm * kHuge.wn * 64, 0, s>>>(a);
@@ -670,7 +670,7 @@ void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t 
 }
 }  // namespace
 
-int grouped_block_rows(int shape) { return kGroupedShapes[std::min(std::max(shape, 0), 5)].bm(); }
+int grouped_block_rows(int shape) { return kGroupedShapes[std::min(std::max(shape, 0), 6)].bm(); }
 
 // Row block for a grouped call, from the average rows per expert. At the Zipf-routed
 // T = 256 block (16 rows per expert on average, the heaviest experts near 250) 32-row tiles
@@ -707,7 +707,7 @@ int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const
                   "problem too large");
     mfma_args a{};
     fill_common(a, x, w, scale, scale_dtype, rows, n, k, block_n, group_size, y);
-    const struct shape sh = kGroupedShapes[std::min(std::max(shape, 0), 5)];
+    const struct shape sh = kGroupedShapes[std::min(std::max(shape, 0), 6)];
     a.splits = 1;
     a.tiles_per_split = a.ktiles;
     a.m_blocks = 1;

@@ -438,7 +438,9 @@ grouped_plan plan_grouped(int64_t rows, int64_t n_experts) {
     grouped_plan p{};
     p.two = rows >= 128 * n_experts;
     if (p.two) {
-        p.shape = 4, p.shape_b = 1;  // 256 x 256 blocks, then 64-row tiles
+        // 256 x 256 blocks on 8 wavefronts of 256 x 32 (each strip dequantized once; 1-2 %
+        // faster at T = 4096 than the 2 x 4 wavefront grid), then 64-row tiles.
+        p.shape = 6, p.shape_b = 1;
         p.bb = 256, p.sb = 64, p.full = 192;
     }
     if (p.two) {
