@@ -379,6 +379,7 @@ struct shape {
 constexpr shape kHuge{2, 4, 8, 4};   // 256 x 256, 8 wavefronts (two stages fill the 160 KiB LDS)
 constexpr shape kWide{2, 4, 8, 3};   // 256 x 192, 8 wavefronts (N = 6144 gives whole rounds)
 constexpr shape kTall{1, 8, 16, 2};  // 256 x 256, 8 wavefronts of 256 x 32: each strip dequantized once
+constexpr shape kTallHalf{1, 8, 8, 2};  // 128 x 256, 8 wavefronts of 128 x 32 (int4 tail launch of kTall)
 constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts
 constexpr shape kLarge8{2, 4, 8, 2};  // 256 x 128, 8 wavefronts of 128 x 32 (plain fp8 W8A16)
 constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
@@ -390,7 +391,7 @@ constexpr shape kRows64w8{1, 8, 4, 1};  // 64 x 128, 8 wavefronts of one strip (
 constexpr shape kRows32{1, 4, 2, 2};  // 32 x 128 (grouped)
 constexpr shape kGroupedShapes[7] = {kRows16, kRows64, kSmall, kLarge, kHuge, kRows32, kTall};
 constexpr shape shape_of(int id) {
-    return id == 9 ? kLarge8 : id == 8 ? kRows64w8 : id == 7 ? kSmall8 : id == 6 ? kTall : id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
+    return id == 10 ? kTallHalf : id == 9 ? kLarge8 : id == 8 ? kRows64w8 : id == 7 ? kSmall8 : id == 6 ? kTall : id == 5 ? kWide : id == 4 ? kRows16 : id == 3 ? kRows64 : id == 2 ? kHuge : id == 1 ? kLarge : kSmall;
 }
 // Relative MFMA throughput per unit of tile area, measured on MI355X at the Qwen3-8B shapes.
 constexpr double kShapeRate[10] = {0.75, 0.7, 1.0, 0.65, 0.3, 0.95, 1.03, 0.8, 0.7, 0.75};
@@ -405,7 +406,16 @@ struct mfma_config {
     // round: the last tail_tiles work tiles run second, with K split tail_splits ways, so
     // the last round is shorter instead of half empty.
     int tail_tiles, tail_splits, tail_tiles_per_split;
+    // int4 on the tall shape, when the tail is whole columns of work tiles: the tail runs
+    // unsplit as 128-row halves of those tiles (shape 10), twice as many workgroups with no
+    // partial sums to combine.
+    bool tail_halves;
 };
+
+bool tail_halves_off() {
+    static const bool off = getenv("PLM_MFMA_NO_HALVES") != nullptr;  // A/B measurements
+    return off;
+}
 
 bool no_tail() {
     static const bool off = getenv("PLM_MFMA_NO_TAIL") != nullptr;  // A/B measurements
@@ -445,6 +455,12 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
             c.tail_tiles_per_split = static_cast<int>(ceil_div(ktiles, ts));
             c.tail_splits = static_cast<int>(ceil_div(ktiles, c.tail_tiles_per_split));
             if (c.tail_splits >= 2) c.tail_tiles = static_cast<int>(rem);
+            if (id == 6 && f == PLM_INT4 && !a8 && rem % c.m_blocks == 0 && !tail_halves_off()) {
+                c.tail_tiles = static_cast<int>(rem);
+                c.tail_halves = true;
+                c.tail_splits = 1;
+                c.tail_tiles_per_split = static_cast<int>(ktiles);
+            }
         }
         return c;
     };
@@ -460,6 +476,10 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
         if (f == PLM_FP8 && !a8 && c.shape == 9) rate = 0.72;
         const double area = static_cast<double>(sh.bm()) * sh.bs() / rate;
         const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
+        if (c.tail_halves) {  // half-area tiles, assumed 10 % less efficient
+            const int64_t full_rounds = (tiles - c.tail_tiles) / cus;
+            return (static_cast<double>(full_rounds) * (c.tiles_per_split + 3) + 0.55 * (ktiles + 3)) * area;
+        }
         if (c.tail_tiles > 0) {
             const int64_t full_rounds = (tiles - c.tail_tiles) / cus;
             return (static_cast<double>(full_rounds) * (c.tiles_per_split + 3) + c.tail_tiles_per_split + 3 +
@@ -490,6 +510,7 @@ int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k, bool
     const mfma_config c = choose_mfma(f, m, n, k, a8);
     const shape sh = shape_of(c.shape);
     const int64_t tile_bytes = static_cast<int64_t>(sh.bm()) * sh.bs() * kTileN * 4;
+    if (c.tail_halves) return 0;
     if (c.tail_tiles > 0) return kCounterBytes + static_cast<int64_t>(c.tail_tiles) * c.tail_splits * tile_bytes;
     if (c.splits <= 1) return 0;
     return kCounterBytes + static_cast<int64_t>(c.m_blocks) * c.n_blocks * c.splits * tile_bytes;
@@ -526,6 +547,11 @@ void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
         if (shape == 7) {
             mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kSmall8.wm, kSmall8.wn, kSmall8.mt, kSmall8.ns>
                 <<<grid, kSmall8.wm * kSmall8.wn * 64, 0, s>>>(a);
+            return;
+        }
+        if (shape == 10) {
+            mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kTallHalf.wm, kTallHalf.wn, kTallHalf.mt, kTallHalf.ns>
+                <<<grid, kTallHalf.wm * kTallHalf.wn * 64, 0, s>>>(a);
             return;
         }
         if (shape == 8) {
@@ -616,7 +642,7 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
     a.n_blocks = c.n_blocks;
     a.xq = xq;
     a.x_scale = x_scale;
-    if (c.splits > 1 || c.tail_tiles > 0) {
+    if (c.splits > 1 || (c.tail_tiles > 0 && !c.tail_halves)) {
         const int64_t need = mfma_workspace_bytes(f, m, n, k, a8);
         if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need) {
             set_error(op, "workspace of %lld bytes required, %zu given", static_cast<long long>(need), workspace_bytes);
@@ -627,6 +653,18 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
     }
     const bool uniform = group_size % kTileK == 0;
     const int tiles = c.m_blocks * c.n_blocks;
+    if (c.tail_halves) {
+        // Whole rounds of tall tiles, then the tail's columns of tiles as 128-row halves.
+        const int nb_full = (tiles - c.tail_tiles) / c.m_blocks;
+        launch_all<false>(f, bf16, a, c.shape, uniform, false, dim3(tiles - c.tail_tiles, 1), s);
+        PLM_HIP_LAUNCH_CHECK(op);
+        const int mb2 = static_cast<int>(ceil_div(m, kTallHalf.bm()));
+        a.m_blocks = mb2;
+        a.tile_base = nb_full * mb2;
+        launch_all<false>(f, bf16, a, 10, uniform, false, dim3((c.n_blocks - nb_full) * mb2, 1), s);
+        PLM_HIP_LAUNCH_CHECK(op);
+        return PLM_OK;
+    }
     if (c.tail_tiles > 0) {
         // Whole rounds of unsplit tiles, then the tail tiles with K split.
         launch_all<false>(f, bf16, a, c.shape, uniform, xq != nullptr, dim3(tiles - c.tail_tiles, 1), s);
