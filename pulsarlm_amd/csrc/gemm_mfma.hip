@@ -379,7 +379,7 @@ struct shape {
 constexpr shape kHuge{2, 4, 8, 4};   // 256 x 256, 8 wavefronts (two stages fill the 160 KiB LDS)
 constexpr shape kWide{2, 4, 8, 3};   // 256 x 192, 8 wavefronts (N = 6144 gives whole rounds)
 constexpr shape kTall{1, 8, 16, 2};  // 256 x 256, 8 wavefronts of 256 x 32: each strip dequantized once
-constexpr shape kTallHalf{1, 8, 8, 2};  // 128 x 256, 8 wavefronts of 128 x 32 (int4 tail launch of kTall)
+constexpr shape kTallHalf{1, 8, 8, 2};  // 128 x 256, 8 wavefronts of 128 x 32 (tail launch of kTall)
 constexpr shape kLarge{2, 2, 8, 4};  // 256 x 128, 4 wavefronts
 constexpr shape kLarge8{2, 4, 8, 2};  // 256 x 128, 8 wavefronts of 128 x 32 (plain fp8 W8A16)
 constexpr shape kSmall{2, 2, 4, 4};  // 128 x 128, 4 wavefronts
@@ -406,7 +406,7 @@ struct mfma_config {
     // round: the last tail_tiles work tiles run second, with K split tail_splits ways, so
     // the last round is shorter instead of half empty.
     int tail_tiles, tail_splits, tail_tiles_per_split;
-    // int4 on the tall shape, when the tail is whole columns of work tiles: the tail runs
+    // The tall shape, when the tail is whole columns of work tiles: the tail runs
     // unsplit as 128-row halves of those tiles (shape 10), twice as many workgroups with no
     // partial sums to combine.
     bool tail_halves;
@@ -455,7 +455,8 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
             c.tail_tiles_per_split = static_cast<int>(ceil_div(ktiles, ts));
             c.tail_splits = static_cast<int>(ceil_div(ktiles, c.tail_tiles_per_split));
             if (c.tail_splits >= 2) c.tail_tiles = static_cast<int>(rem);
-            if (id == 6 && f == PLM_INT4 && !a8 && rem % c.m_blocks == 0 && !tail_halves_off()) {
+            // (fp8 W8A16, whose tall shape keeps the weights in registers, measured slower.)
+            if (id == 6 && (f == PLM_INT4 || a8) && rem % c.m_blocks == 0 && !tail_halves_off()) {
                 c.tail_tiles = static_cast<int>(rem);
                 c.tail_halves = true;
                 c.tail_splits = 1;
@@ -656,12 +657,12 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
     if (c.tail_halves) {
         // Whole rounds of tall tiles, then the tail's columns of tiles as 128-row halves.
         const int nb_full = (tiles - c.tail_tiles) / c.m_blocks;
-        launch_all<false>(f, bf16, a, c.shape, uniform, false, dim3(tiles - c.tail_tiles, 1), s);
+        launch_all<false>(f, bf16, a, c.shape, uniform, a8, dim3(tiles - c.tail_tiles, 1), s);
         PLM_HIP_LAUNCH_CHECK(op);
         const int mb2 = static_cast<int>(ceil_div(m, kTallHalf.bm()));
         a.m_blocks = mb2;
         a.tile_base = nb_full * mb2;
-        launch_all<false>(f, bf16, a, 10, uniform, false, dim3((c.n_blocks - nb_full) * mb2, 1), s);
+        launch_all<false>(f, bf16, a, 10, uniform, a8, dim3((c.n_blocks - nb_full) * mb2, 1), s);
         PLM_HIP_LAUNCH_CHECK(op);
         return PLM_OK;
     }

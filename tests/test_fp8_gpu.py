@@ -88,3 +88,30 @@ def test_w8a8_rejects_small_groups():
                                         torch.ones((1, 4), device="cuda"), 128, 64)
     with pytest.raises(RuntimeError, match="gemm_fp8_w8a8: group_size must be a multiple of 128"):
         ops.gemm_fp8_w8a8_cuda(torch.zeros((4, 256), dtype=torch.bfloat16, device="cuda"), wt, st, 64, 128, 64)
+
+
+def test_w8a8_full_size_tall_tail():
+    """W8A8 at the config-4 gate_up shape (M=2048, K=5120, N=34816): 1088 tall 256x256 tiles,
+    whose last 64 (whole tile columns) run as 128-row halves in a second launch. Checked
+    against a GPU fp32 reference of the same arithmetic: per-token e4m3 x times its row
+    scale, e4m3 weights times their 128x128 block scale. The products are exact, so the
+    only differences are fp32 summation order and the bf16 output rounding."""
+    m, k, n = 2048, 5120, 34816
+    g = torch.Generator(device="cpu").manual_seed(91)
+    codes = torch.randint(0, 256, (n, k), generator=g, dtype=torch.int32).to(torch.uint8)
+    codes[(codes == 0x7F) | (codes == 0xFF)] = 0  # no NaN codes
+    scale = (torch.rand((n // 128, k // 128), generator=g) * 0.1 + 0.01).float()
+    x = torch.randn((m, k), generator=g).bfloat16().cuda()
+    wt, st = ops.repack_fp8_marlin_cuda(codes.cuda().view(torch.float8_e4m3fn), scale.cuda(), 128, 128)
+    y = ops.gemm_fp8_w8a8_cuda(x, wt, st, n, 128, 128)
+    xq, sx = ops.quantize_rows_e4m3_cuda(x)
+    xf = xq.view(torch.float8_e4m3fn).float() * sx[:, None]
+    wf = codes.cuda().view(torch.float8_e4m3fn).float()
+    wf *= scale.cuda().repeat_interleave(128, 0).repeat_interleave(128, 1)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ref = xf @ wf.T
+    del wf
+    err = (y.float() - ref).abs()
+    assert bool((err <= 2.0**-8 * ref.abs() + 1e-3 * ref.abs().max()).all()), f"max err {err.max().item():.4g}"
+    rel = (torch.linalg.vector_norm(y.float() - ref) / torch.linalg.vector_norm(ref)).item()
+    assert rel <= 5e-3, rel
