@@ -62,6 +62,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=24)
     p.add_argument("--warmup", type=int, default=6)
+    # Exactly these counts are run and reported (a partial last pass over the copies is fine).
     p.add_argument("--quick", action="store_true", help="decode headline only")
     p.add_argument("--only", choices=["decode", "prefill", "fp8", "moe", "copy", "crossover"], default=None)
     p.add_argument("--m", default="1,2,4,8,12,16,24,32,48,64", help="M values of --only crossover")
@@ -163,6 +164,51 @@ class Bench:
                                             GROUP, y.data_ptr(), ws, wsn, st))
 
 
+def time_steps(b: Bench, launches_for_copies, copies, steps, warmup):
+    """Seconds per step over exactly `steps` timed steps after exactly `warmup` untimed
+    ones. launches_for_copies(r) gives the launches of the first r steps of a pass over
+    the weight copies (step i reads copy i % copies); the step count wraps the pass."""
+    torch = b.torch
+    graphs = {}
+
+    def runner(r):
+        if r not in graphs:
+            launches = launches_for_copies(r)
+            if b.eager:
+                graphs[r] = lambda: [f() for f in launches]
+            else:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=b.stream):
+                    for f in launches:
+                        f()
+                graphs[r] = g.replay
+        return graphs[r]
+
+    def run(n):
+        for _ in range(n // copies):
+            runner(copies)()
+        if n % copies:
+            runner(n % copies)()
+
+    with torch.cuda.stream(b.stream):
+        for f in launches_for_copies(copies):  # eager first calls (per-stream set-up), not counted
+            f()
+        b.stream.synchronize()
+        runner(copies)
+        if steps % copies:
+            runner(steps % copies)
+        if warmup % copies:
+            runner(warmup % copies)
+        run(warmup)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(b.stream)
+        run(steps)
+        e1.record(b.stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / max(steps, 1)
+
+
 def section_decode(b: Bench, steps, warmup, detail_shapes=True):
     torch, L = b.torch, b._lib
     layers = {name: b.int4_layer(k, n, i, min_copies=6) for i, (name, k, n) in enumerate(SHAPES)}
@@ -182,12 +228,13 @@ def section_decode(b: Bench, steps, warmup, detail_shapes=True):
                     out.append(b.gemm_launch(L.PLM_INT4, xs[(m, k)], w, s, L.PLM_FP16, m, n, k, 1, ys[(m, n)]))
         return out
 
-    # Headline: the 12-GEMM step, rotated over 6 copies of the layer set (~600 MB).
+    # Headline: the 12-GEMM step, rotated over 6 copies of the layer set (~600 MB). Exactly
+    # `warmup` untimed steps, then exactly `steps` timed ones: whole passes over the copies
+    # replay one graph, and a last partial pass replays a graph of its first r steps.
     copies = 6
-    reps = max(1, -(-steps // copies))
-    t_pass = b.time(launches_for({s[0] for s in SHAPES}, DECODE_M, copies), reps=reps, warm=max(1, warmup // copies))
+    t_step = time_steps(b, lambda r: launches_for({s[0] for s in SHAPES}, DECODE_M, r),
+                        copies, steps, warmup)
     step_bytes = sum(w4a16_bytes(m, n, k) for (_, k, n) in SHAPES for m in DECODE_M)
-    t_step = t_pass / copies
     detail = {}
     for name, k, n in (SHAPES if detail_shapes else []):
         for m in DECODE_M:
@@ -199,8 +246,8 @@ def section_decode(b: Bench, steps, warmup, detail_shapes=True):
     launches_per_step = len(SHAPES) * len(DECODE_M)
     return {
         "value": step_bytes / t_step / 1e9,
-        "steps": reps * copies,
-        "warmup": max(1, warmup // copies) * copies,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": t_step * 1e3,
         "per_launch_bytes": step_bytes / launches_per_step,
         "avg_launch_s": t_step / launches_per_step,

@@ -69,7 +69,7 @@ int64_t plm_scale_bytes(int64_t n, int64_t k, int64_t block_n, int64_t group_siz
 
 /*
  * Repack int4 weights for the GEMMs.
- * Replaces repack_int4_marlin_cuda (pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:317-322,
+ * Replaces repack_int4_marlin_cuda (pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:306-311,
  * pulsarlm-core/src/kernels/marlin.cu:601-620).
  *   weight_packed  int32 [N, K/8], 8 signed nibbles per int32 along K, least significant first
  *   weight_scale   [ceil(N/block_n), K/group_size] in scale_dtype, row-major
@@ -81,7 +81,7 @@ int plm_repack_int4(const int32_t* weight_packed, const void* weight_scale, plm_
                     int64_t n, int64_t k, int64_t block_n, int64_t group_size,
                     void* weight_out, void* scale_out, void* stream);
 
-/* Repack e4m3 weights [N, K] (bytes). Replaces repack_fp8_marlin_cuda (ops.hpp:324-325,
+/* Repack e4m3 weights [N, K] (bytes). Replaces repack_fp8_marlin_cuda (ops.hpp:313-314,
  * marlin.cu:622-629). */
 int plm_repack_fp8(const uint8_t* weight, const void* weight_scale, plm_dtype scale_dtype,
                    int64_t n, int64_t k, int64_t block_n, int64_t group_size,
@@ -111,7 +111,7 @@ int64_t plm_gemm_workspace_bytes(plm_format format, int64_t m, int64_t n, int64_
 /*
  * y [M, N] = x [M, K] @ dequant(W)^T, x and y in x_dtype (PLM_BF16 or PLM_FP16),
  * fp32 accumulation. Replaces gemm_int4_marlin_cuda / gemm_fp8_marlin_cuda
- * (ops.hpp:327-343, marlin.cu:538-597,631-651).
+ * (ops.hpp:316-332, marlin.cu:538-597,631-651).
  * M <= 16 (and up to 32 rows where measured faster) runs the bandwidth-first decode kernels;
  * larger M the MFMA kernel.
  * M == 0 or N == 0 returns PLM_OK without touching y.
@@ -154,6 +154,10 @@ int plm_gemm_w8a8(const void* x, plm_dtype x_dtype,
  * back (plm_weight_bytes each), scale likewise (plm_scale_bytes each).
  * Replaces one at::_grouped_mm(rows, W^T, offsets) call of routed_experts
  * (paged_forward.cpp:124-125) for int4 experts (PLM_INT4 only).
+ * The offsets are expected to be non-decreasing with offsets[n_experts-1] == rows.
+ * Others are clamped on the device: each expert's rows are [clamp(offsets[e-1]),
+ * max(clamp(offsets[e]), clamp(offsets[e-1]))) with clamp to [0, rows], so no tile
+ * reads or writes outside rows [0, rows); rows no expert covers are not written.
  */
 int plm_grouped_gemm(plm_format format, const void* x, plm_dtype x_dtype,
                      const void* weight, const void* scale, plm_dtype scale_dtype,
@@ -172,6 +176,9 @@ int64_t plm_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t n_experts
  * routed_experts (paged_forward.cpp:108-130) for int4 experts and SiLU:
  *   out [T, H] = sum_j top_weights[t, j] * down_e(silu(g) * u), (g | u) = gate_up_e(h[t]),
  * e = top_experts[t, j] (int32 [T, top_k]), top_weights fp32 [T, top_k].
+ * Assignments whose expert id lies outside [0, n_experts) (e.g. -1 padding) are
+ * dropped: they add nothing to their token's sum and are not counted in offsets.
+ * (The reference's index_add_ would raise on them.)
  * gate_up holds n_experts repacked [2I, H] weights, down n_experts [H, I].
  * Sorting by expert, offsets, gather, both grouped GEMMs, the activation and the
  * weighted scatter-back all run on the device with no host synchronization.
@@ -212,7 +219,7 @@ int plm_silu_mul(const void* x, plm_dtype dtype, int64_t tokens, int64_t n, void
  * read in place (no repack). num_splits = 0 picks the K split; >= 1 forces it (the extra
  * splits past the K tiles contribute zero). The split partials go to the workspace
  * (plm_gemm_int4_plain_workspace_bytes; no zeroing needed) and are summed in split order.
- * Replaces gemm_int4_cuda / gemm_int4_split_cuda (ops.hpp:269-297, int4_gemm.cu:153-478).
+ * Replaces gemm_int4_cuda / gemm_int4_split_cuda (ops.hpp:272-297, int4_gemm.cu:153-478).
  */
 int64_t plm_gemm_int4_plain_workspace_bytes(int64_t m, int64_t n, int64_t k, int64_t num_splits);
 int plm_gemm_int4_plain(const void* x, plm_dtype x_dtype, const int32_t* weight_packed, const float* weight_scale,

@@ -13,7 +13,7 @@ path in pulsarlm-core:
 
 * int4 packing, 8 signed nibbles per int32 along K, least significant first
   (``pulsarlm-core/tests/kernels/test_marlin.cpp:42-46``,
-  ``pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:317-322``);
+  ``pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:306-311``);
 * dequantization ``W = round(q * round(scale))`` in the activation dtype, i.e.
   ``weight.to(dtype) * expanded_scale.to(dtype)`` (``test_marlin.cpp:48-50``),
   which is what the kernel's ``scale_pair`` + ``__hmul2`` compute
@@ -44,15 +44,24 @@ How each function is pinned (checks live in ``tests/test_oracle.py``):
 * ``marlin_encode_*``: known answers derived by hand from the lane/offset
   description at ``marlin.cu:21-30,86-88,154-155``, and decode(encode(W)) == W.
 * ``gemm_ref``: against torch fp32 matmul, and the identity-GEMM closed form.
-* ``routed_experts_ref``: against the per-expert dense restatement.
+* ``routed_experts_ref``: each rounding point (gate_up output, act(g)*u, down
+  output, weighted term) against the reference's own steps
+  (``paged_forward.cpp:116-129``: stable argsort, index_add_ counts, cumsum,
+  ``at::_grouped_mm`` twice, silu, ``down * w.to(dtype)``, ``index_add_``) evaluated
+  by torch on the CPU in bf16; order and offsets exactly; the summed output within
+  the MoE tolerance; and against the per-expert dense restatement.
 * ``fp8_block_quantize``: invariants (one code per block at |448|, exact
   reconstruction bound) and against torch's e4m3 cast.
 * ``route_top_k_ref``: torch's softmax and topk (the reference test's own checks,
   ``pulsarlm-core/tests/kernels/test_fused_ops.cpp:83-100``) and hand-derived
   tie-breaking cases.
 * ``silu_mul_ref``: torch's silu on a sweep, and the closed forms at 0 and large |g|.
-* ``quantize_per_token_e4m3`` (W8A8 mode): parity unpinned by the reference,
-  which has no fp8-activation path; checked only against torch's e4m3 cast.
+* ``quantize_per_token_e4m3`` (W8A8 mode): codes and scales bit for bit against
+  the reference's quantizer expression (``test_qwen3_5.cpp:301-311``: fp32
+  ``amax.clamp_min(1e-12) / 448``, fp32 divide, torch ``float8_e4m3fn`` cast) applied
+  per row by torch, on rows with zeros, ties, tiny and huge amax.
+* ``gemm_w8a8_ref``: against a torch float64 matmul of the ``float8_e4m3fn``
+  casts times their scales.
 """
 
 from __future__ import annotations
@@ -138,7 +147,7 @@ def e4m3_encode(x) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
-# int4 packing (test_marlin.cpp:42-46; ops.hpp:317-322)
+# int4 packing (test_marlin.cpp:42-46; ops.hpp:306-311)
 # ---------------------------------------------------------------------------
 
 
@@ -338,8 +347,9 @@ def fp8_block_quantize(w, block_n: int = 128, block_k: int = 128):
 
 
 def quantize_per_token_e4m3(x):
-    """W8A8 activation quantizer (no reference counterpart; parity unpinned by the
-    reference): per row, scale = max(amax, 1e-12)/448, codes = e4m3(x/scale)."""
+    """W8A8 activation quantizer: the block quantizer of test_qwen3_5.cpp:301-311
+    applied per row (one 1 x K block per token): scale = max(amax, 1e-12) / 448 in
+    fp32, codes = e4m3_rne(x / scale) with an fp32 divide."""
     x = np.asarray(x, dtype=np.float32)
     amax = np.abs(x).max(axis=1) if x.size else np.zeros((x.shape[0],), np.float32)
     scale = (np.maximum(amax, np.float32(1e-12)) / np.float32(448.0)).astype(np.float32)
@@ -348,7 +358,8 @@ def quantize_per_token_e4m3(x):
 
 
 def gemm_w8a8_ref(codes_x, scale_x, codes_w, scale_w, block_n: int, group_size: int, dtype="bf16"):
-    """y = diag(sx) * e4m3(cx) @ (e4m3(cw) * s_w)^T, exact products, float64 sums."""
+    """y = diag(sx) * e4m3(cx) @ (e4m3(cw) * s_w)^T, exact products, float64 sums,
+    rounded once to ``dtype``."""
     xq = e4m3_decode(codes_x).astype(np.float64) * np.asarray(scale_x, np.float64)[:, None]
     n, k = np.asarray(codes_w).shape
     wq = e4m3_decode(codes_w).astype(np.float64) * expand_scale(scale_w, n, k, block_n, group_size)
@@ -378,20 +389,27 @@ def moe_sort(top_experts, n_experts: int):
     return order, tokens, counts, offsets
 
 
-def routed_experts_ref(h, top_experts, top_weights, gate_up, down, dtype="bf16"):
+def routed_experts_ref(h, top_experts, top_weights, gate_up, down, dtype="bf16", parts=False):
     """Restatement of routed_experts with dense per-expert weights (already
     dequantized): gate_up [E, 2I, H], down [E, H, I], with the reference's
     rounding points in the activation dtype: each grouped GEMM's output
     (accumulated here in float64), at::silu(g), its product with u, and each
     weighted term down * top_weight.to(dtype) (paged_forward.cpp:124-128). The
     reference's index_add_ accumulates those terms in the activation dtype in a
-    scheduling-dependent order; here they are summed in float64 and rounded once."""
+    scheduling-dependent order; here they are summed in float64 and rounded once.
+
+    With ``parts=True`` it also returns the per-row stages in sorted order
+    (gate_up output, act(g)*u, down output, weighted term), one per rounding point,
+    so each can be compared with the reference's own steps."""
     h = np.asarray(h, dtype=np.float32)
     e_count = gate_up.shape[0]
     inter = gate_up.shape[1] // 2
     order, tokens, counts, offsets = moe_sort(top_experts, e_count)
     wflat = np.asarray(top_weights, dtype=np.float32).reshape(-1)[order]
     rows = h[tokens]
+    n_rows = rows.shape[0]
+    stages = {"gate_up": np.zeros((n_rows, 2 * inter), np.float32), "act": np.zeros((n_rows, inter), np.float32),
+              "down": np.zeros((n_rows, h.shape[1]), np.float32), "weighted": np.zeros((n_rows, h.shape[1]), np.float32)}
     out = np.zeros(h.shape, dtype=np.float64)
     start = 0
     for e in range(e_count):
@@ -403,8 +421,13 @@ def routed_experts_ref(h, top_experts, top_weights, gate_up, down, dtype="bf16")
             d = gemm_ref(act, down[e], dtype)
             term = round_to(d * round_to(wflat[start:end], dtype)[:, None], dtype)
             np.add.at(out, tokens[start:end], term.astype(np.float64))
+            for name, v in (("gate_up", gu), ("act", act), ("down", d), ("weighted", term)):
+                stages[name][start:end] = v
         start = end
-    return round_to(out.astype(np.float32), dtype)
+    result = round_to(out.astype(np.float32), dtype)
+    if parts:
+        return result, dict(stages, order=order, offsets=offsets)
+    return result
 
 
 def sparse_moe_ref(h, top_experts, top_weights, gate_up, down, dtype="bf16"):

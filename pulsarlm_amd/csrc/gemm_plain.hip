@@ -3,7 +3,7 @@
 // first) and scale fp32 [N, K/g].
 //
 // Counterpart of gemm_int4_cuda / gemm_int4_split_cuda (pulsarlm-core/inc/pulsarlm/kernels/
-// ops.hpp:269-297, pulsarlm-core/src/kernels/int4_gemm.cu:53-57,136-138,153-478), which the
+// ops.hpp:272-297, pulsarlm-core/src/kernels/int4_gemm.cu:53-57,136-138,153-478), which the
 // reference declares but never calls (its engine runs the repacked path). Kept simple, not
 // tuned, with the reference's rounding (the product rounded to fp32, then to x's dtype):
 //

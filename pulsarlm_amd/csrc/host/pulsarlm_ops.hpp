@@ -3,7 +3,7 @@
 //
 // The first four functions keep the exact signatures, argument meaning and error
 // behaviour (TORCH_CHECK -> c10::Error, "<op>: ..." messages, empty [M, N] for
-// M == 0 or N == 0) of pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:317-343, so a
+// M == 0 or N == 0) of pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:306-332, so a
 // caller such as linear (pulsarlm-core/src/engine/model/linear.cpp:19-41) links
 // against this file instead of marlin.cu. Work is enqueued on the current HIP stream
 // of the tensors' device; nothing synchronizes. weight_marlin / scale_marlin are
@@ -17,20 +17,20 @@
 
 namespace pulsarlm {
 
-// ops.hpp:317-322
+// ops.hpp:306-311
 std::tuple<at::Tensor, at::Tensor> repack_int4_marlin_cuda(const at::Tensor& weight_packed,
                                                            const at::Tensor& weight_scale, int64_t block_n,
                                                            int64_t group_size);
 
-// ops.hpp:324-325
+// ops.hpp:313-314
 std::tuple<at::Tensor, at::Tensor> repack_fp8_marlin_cuda(const at::Tensor& weight, const at::Tensor& weight_scale,
                                                           int64_t block_n, int64_t group_size);
 
-// ops.hpp:327-334
+// ops.hpp:316-323
 at::Tensor gemm_int4_marlin_cuda(const at::Tensor& x, const at::Tensor& weight_marlin, const at::Tensor& scale_marlin,
                                  int64_t n, int64_t block_n, int64_t group_size);
 
-// ops.hpp:336-343
+// ops.hpp:325-332
 at::Tensor gemm_fp8_marlin_cuda(const at::Tensor& x, const at::Tensor& weight_marlin, const at::Tensor& scale_marlin,
                                 int64_t n, int64_t block_n, int64_t group_size);
 
@@ -80,7 +80,7 @@ std::tuple<at::Tensor, at::Tensor> route_top_k_cuda(const at::Tensor& logits, in
 // silu_mul_cuda (ops.hpp:42-43): silu(x[:, :n]) * x[:, n:], silu rounded to the dtype.
 at::Tensor silu_mul_cuda(const at::Tensor& x);
 
-// gemm_int4_cuda / gemm_int4_split_cuda (pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:269-297):
+// gemm_int4_cuda / gemm_int4_split_cuda (pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:272-297):
 // y [M, N] = x @ W^T with W = round(fp32(q * scale)) from weight_packed int32 [N, K/8] and
 // weight_scale fp32 [N, K/group_size], read in place; the split variant forces num_splits.
 at::Tensor gemm_int4_cuda(const at::Tensor& x, const at::Tensor& weight_packed, const at::Tensor& weight_scale,

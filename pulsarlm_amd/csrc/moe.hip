@@ -118,7 +118,11 @@ __global__ void __launch_bounds__(kChunk) moe_scatter_kernel(const int32_t* __re
     const int e = a < total ? experts[a] : -1;
     chunk_experts[threadIdx.x] = e;
     __syncthreads();
-    if (a >= total || e < 0 || e >= n_experts) return;
+    if (a >= total) return;
+    if (e < 0 || e >= n_experts) {  // dropped: the combine skips it
+        position[a] = -1;
+        return;
+    }
     int rank = 0;
     for (int j = 0; j < static_cast<int>(threadIdx.x); ++j) rank += chunk_experts[j] == e;
     const int32_t pos = start[e] + chunk_base[static_cast<int64_t>(blockIdx.x) * n_experts + e] + rank;
@@ -127,22 +131,34 @@ __global__ void __launch_bounds__(kChunk) moe_scatter_kernel(const int32_t* __re
     position[a] = pos;
 }
 
+// Expert e's rows [lo, hi) from caller-supplied inclusive-end offsets, clamped to
+// [0, rows] and to hi >= lo, so offsets that are not a non-decreasing cumsum ending at
+// `rows` cannot send tiles past the rows the caller sized x, y and the tile slots for.
+__device__ __forceinline__ void expert_rows(const int32_t* __restrict__ offsets, int e, int32_t rows, int32_t& lo,
+                                            int32_t& hi) {
+    lo = e == 0 ? 0 : min(max(offsets[e - 1], 0), rows);
+    hi = max(min(max(offsets[e], 0), rows), lo);
+}
+
 // Tile list for the grouped GEMM: expert e's rows [off[e-1], off[e]) in blocks of bm,
 // written at the expert's tile prefix; slots past the last tile get rows = 0.
-__global__ void __launch_bounds__(1024) moe_tiles_kernel(const int32_t* __restrict__ offsets, int n_experts, int bm,
-                                                          int64_t max_tiles, int32_t* __restrict__ tiles) {
+__global__ void __launch_bounds__(1024) moe_tiles_kernel(const int32_t* __restrict__ offsets, int n_experts,
+                                                          int32_t rows, int bm, int64_t max_tiles,
+                                                          int32_t* __restrict__ tiles) {
     __shared__ int32_t buf[1024];
     __shared__ int32_t first_tile[4096];
     for (int e = threadIdx.x; e < n_experts; e += 1024) {
-        const int32_t rows = offsets[e] - (e == 0 ? 0 : offsets[e - 1]);
-        first_tile[e] = rows > 0 ? (rows + bm - 1) / bm : 0;
+        int32_t lo, hi;
+        expert_rows(offsets, e, rows, lo, hi);
+        first_tile[e] = (hi - lo + bm - 1) / bm;
     }
     __syncthreads();
     const int32_t n_tiles = block_exclusive_scan(first_tile, n_experts, buf);
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
-        const int32_t lo = e == 0 ? 0 : offsets[e - 1], hi = offsets[e];
+        int32_t lo, hi;
+        expert_rows(offsets, e, rows, lo, hi);
         int32_t t = first_tile[e];
-        for (int32_t r = lo; r < hi; r += bm, ++t) {
+        for (int32_t r = lo; r < hi && t < max_tiles; r += bm, ++t) {
             tiles[3 * t] = e;
             tiles[3 * t + 1] = r;
             tiles[3 * t + 2] = min(bm, hi - r);
@@ -256,9 +272,12 @@ __global__ void __launch_bounds__(1024) moe_sort_small_kernel(
     }
 #pragma unroll
     for (int j = 0; j < kPerWave; ++j) {
-        if (ex[j] < 0) continue;
         const int c = wave + 16 * j;
         const int a = c * 64 + lane;
+        if (ex[j] < 0) {  // dropped (out-of-range expert): the combine skips it
+            if (c < n_chunks && a < rows) position[a] = -1;
+            continue;
+        }
         const int32_t pos = tab[ex[j] * n_chunks + c] + rk[j];
         sorted_token[pos] = a / top_k;
         sorted_weight[pos] = wt[j];
@@ -302,15 +321,16 @@ __device__ __forceinline__ void tiles2_split(int32_t c, int bb, int full, int32_
 }
 
 __global__ void __launch_bounds__(1024) moe_tiles2_kernel(const int32_t* __restrict__ offsets, int n_experts,
-                                                           int bb, int sb, int full, int64_t max_big,
+                                                           int32_t rows, int bb, int sb, int full, int64_t max_big,
                                                            int64_t max_small, int32_t* __restrict__ big,
                                                            int32_t* __restrict__ small) {
     __shared__ int32_t buf[1024];
     __shared__ int32_t first_big[4096];
     __shared__ int32_t first_small[4096];
     for (int e = threadIdx.x; e < n_experts; e += 1024) {
-        int32_t nbig, rem;
-        tiles2_split(offsets[e] - (e == 0 ? 0 : offsets[e - 1]), bb, full, nbig, rem);
+        int32_t nbig, rem, lo, hi;
+        expert_rows(offsets, e, rows, lo, hi);
+        tiles2_split(hi - lo, bb, full, nbig, rem);
         first_big[e] = nbig;
         first_small[e] = (rem + sb - 1) / sb;
     }
@@ -318,17 +338,18 @@ __global__ void __launch_bounds__(1024) moe_tiles2_kernel(const int32_t* __restr
     const int32_t n_big = block_exclusive_scan(first_big, n_experts, buf);
     const int32_t n_small = block_exclusive_scan(first_small, n_experts, buf);
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
-        const int32_t lo = e == 0 ? 0 : offsets[e - 1], hi = offsets[e];
-        int32_t nbig, rem;
+        int32_t nbig, rem, lo, hi;
+        expert_rows(offsets, e, rows, lo, hi);
         tiles2_split(hi - lo, bb, full, nbig, rem);
         int32_t r = lo, t = first_big[e];
-        for (int b = 0; b < nbig; ++b, ++t, r += bb) {
+        for (int b = 0; b < nbig && t < max_big; ++b, ++t, r += bb) {
             big[3 * t] = e;
             big[3 * t + 1] = r;
             big[3 * t + 2] = min(bb, hi - r);
         }
+        r = lo + nbig * bb;  // where the big blocks end, also when their slots ran out
         t = first_small[e];
-        for (; r < hi; r += sb, ++t) {
+        for (; r < hi && t < max_small; r += sb, ++t) {
             small[3 * t] = e;
             small[3 * t + 1] = r;
             small[3 * t + 2] = min(sb, hi - r);
@@ -378,6 +399,7 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const uint16_t* __rest
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < top_k; ++j) {
         const int32_t p = position[t * top_k + j];
+        if (p < 0) continue;  // an assignment to an expert id outside [0, n_experts)
         const float w = round_to<BF16>(weights[t * top_k + j]);
         const u32x4_t v = *reinterpret_cast<const u32x4_t*>(d + static_cast<int64_t>(p) * hidden + h);
 #pragma unroll
@@ -484,13 +506,14 @@ int launch_sort(const char* op, const int32_t* experts, const float* weights, in
     return PLM_OK;
 }
 
-int launch_tiles(const char* op, const int32_t* offsets, int64_t n_experts, const grouped_plan& p, int32_t* tiles,
-                 hipStream_t s) {
+int launch_tiles(const char* op, const int32_t* offsets, int64_t n_experts, int64_t rows, const grouped_plan& p,
+                 int32_t* tiles, hipStream_t s) {
     if (p.two)
-        moe_tiles2_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), p.bb, p.sb, p.full, p.max_a, p.max_b, tiles,
+        moe_tiles2_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), int32_t(rows), p.bb, p.sb, p.full, p.max_a, p.max_b, tiles,
                                              tiles + 3 * p.max_a);
     else
-        moe_tiles_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), grouped_block_rows(p.shape), p.max_a, tiles);
+        moe_tiles_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), int32_t(rows), grouped_block_rows(p.shape),
+                                            p.max_a, tiles);
     PLM_HIP_LAUNCH_CHECK(op);
     return PLM_OK;
 }
@@ -539,7 +562,7 @@ int plm_grouped_gemm(plm_format format, const void* x, plm_dtype x_dtype, const 
     }
     auto* tiles = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + kCounterBytes);
     hipStream_t s = as_stream(stream);
-    if (int rc = launch_tiles(op, offsets, n_experts, p, tiles, s)) return rc;
+    if (int rc = launch_tiles(op, offsets, n_experts, rows, p, tiles, s)) return rc;
     return launch_plan(op, p, x, x_dtype == PLM_BF16, weight, scale, scale_dtype, rows, n, k, block_n, group_size, y,
                        tiles, nullptr, s);
 }
@@ -598,7 +621,7 @@ int plm_moe(const void* h, plm_dtype dtype, const int32_t* top_experts, const fl
         PLM_HIP_LAUNCH_CHECK(op);
     } else {
         if (int rc = launch_sort(op, top_experts, top_weights, rows, top_k, n_experts, base, l, offsets, s)) return rc;
-        if (int rc = launch_tiles(op, offsets, n_experts, p, tiles, s)) return rc;
+        if (int rc = launch_tiles(op, offsets, n_experts, rows, p, tiles, s)) return rc;
     }
     // gate_up: [rows, 2I] = h[sorted_token] @ gate_up_e^T
     if (int rc = launch_plan(op, p, h, bf16, gate_up_weight, gate_up_scale, scale_dtype, rows, 2 * intermediate,

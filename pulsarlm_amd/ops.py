@@ -1,7 +1,7 @@
 """Tensor-level ops over the C ABI, mirroring pulsarlm-core's quant-linear ops.
 
 Same names, argument meaning and error behaviour as the reference's
-``pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:299-343``:
+``pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:299-332``:
 
 * ``repack_int4_marlin_cuda(weight_packed, weight_scale, block_n, group_size)``
   -> ``(weight_marlin, scale_marlin)``
@@ -104,7 +104,7 @@ def _repack(op: str, fmt: int, weight: torch.Tensor, n: int, k: int, weight_scal
 
 def repack_int4_marlin_cuda(weight_packed: torch.Tensor, weight_scale: torch.Tensor, block_n: int, group_size: int):
     """int32 [N, K/8] LSB-first int4 + scales [ceil(N/bn), K/g] -> (weight, scale) in the plm layout
-    (ops.hpp:317-322; marlin.cu:601-620)."""
+    (ops.hpp:306-311; marlin.cu:601-620)."""
     _require(weight_packed.dtype == torch.int32 and weight_packed.dim() == 2, "repack_int4_marlin",
              "weight_packed must be int32 [N, K/8]")
     n, k = weight_packed.shape[0], weight_packed.shape[1] * 8
@@ -112,7 +112,7 @@ def repack_int4_marlin_cuda(weight_packed: torch.Tensor, weight_scale: torch.Ten
 
 
 def repack_fp8_marlin_cuda(weight: torch.Tensor, weight_scale: torch.Tensor, block_n: int, group_size: int):
-    """float8_e4m3fn [N, K] + scales -> (weight, scale) in the plm layout (ops.hpp:324-325; marlin.cu:622-629)."""
+    """float8_e4m3fn [N, K] + scales -> (weight, scale) in the plm layout (ops.hpp:313-314; marlin.cu:622-629)."""
     _require(weight.dtype == torch.float8_e4m3fn and weight.dim() == 2, "repack_fp8_marlin",
              "weight must be float8_e4m3fn [N, K]")
     n, k = weight.shape
@@ -188,12 +188,12 @@ def _gemm(op: str, fmt: int, x, weight_marlin, scale_marlin, n: int, block_n: in
 
 
 def gemm_int4_marlin_cuda(x, weight_marlin, scale_marlin, n: int, block_n: int, group_size: int, out=None):
-    """y [M, N] = x [M, K] @ dequant(W)^T (ops.hpp:327-334; marlin.cu:631-640)."""
+    """y [M, N] = x [M, K] @ dequant(W)^T (ops.hpp:316-323; marlin.cu:631-640)."""
     return _gemm("gemm_int4_marlin", _lib.PLM_INT4, x, weight_marlin, scale_marlin, n, block_n, group_size, out)
 
 
 def gemm_fp8_marlin_cuda(x, weight_marlin, scale_marlin, n: int, block_n: int, group_size: int, out=None):
-    """fp8 W8A16 form (ops.hpp:336-343; marlin.cu:642-651)."""
+    """fp8 W8A16 form (ops.hpp:325-332; marlin.cu:642-651)."""
     return _gemm("gemm_fp8_marlin", _lib.PLM_FP8, x, weight_marlin, scale_marlin, n, block_n, group_size, out)
 
 
@@ -362,7 +362,7 @@ def _gemm_int4_plain(op: str, x: torch.Tensor, weight_packed: torch.Tensor, weig
 
 
 def gemm_int4_cuda(x: torch.Tensor, weight_packed: torch.Tensor, weight_scale: torch.Tensor, group_size: int):
-    """gemm_int4_cuda (ops.hpp:269-285): the non-repacked int4 GEMM, W = round(fp32(q * scale))."""
+    """gemm_int4_cuda (ops.hpp:272-285): the non-repacked int4 GEMM, W = round(fp32(q * scale))."""
     return _gemm_int4_plain("gemm_int4", x, weight_packed, weight_scale, group_size, 0)
 
 

@@ -115,3 +115,22 @@ def test_w8a8_full_size_tall_tail():
     assert bool((err <= 2.0**-8 * ref.abs() + 1e-3 * ref.abs().max()).all()), f"max err {err.max().item():.4g}"
     rel = (torch.linalg.vector_norm(y.float() - ref) / torch.linalg.vector_norm(ref)).item()
     assert rel <= 5e-3, rel
+
+
+@pytest.mark.parametrize("shape", [(5120, 7168), (5120, 5120), (5120, 34816), (17408, 5120)])
+def test_config4_w8a16_m2048_every_row(shape):
+    """Config 4, W8A16 at M=2048, every row of every shape: the weights come from
+    plm_dequant (bit-exact, pinned against the oracle) and the reference product is
+    torch's fp32 matmul of the rounded operands on the GPU. gate_up runs the tall
+    register-weight tiles with the K-split tail launch."""
+    from tests.test_gemm_gpu import _check_full
+    k, n = shape
+    g = torch.Generator(device="cpu").manual_seed(k + n)
+    codes = torch.randint(0, 256, (n, k), generator=g, dtype=torch.int32).to(torch.uint8)
+    codes[(codes == 0x7F) | (codes == 0xFF)] = 0
+    scale = (torch.rand((n // 128, k // 128), generator=g) * 0.02 + 1e-3).float()
+    x = torch.randn((2048, k), generator=g).bfloat16().cuda()
+    wt, st = ops.repack_fp8_marlin_cuda(codes.cuda().view(torch.float8_e4m3fn), scale.cuda(), 128, 128)
+    wd = ops.dequant_marlin_cuda("fp8", wt, st, n, k, 128, 128)
+    y = ops.gemm_fp8_marlin_cuda(x, wt, st, n, 128, 128)
+    print(shape, "rel-L2", _check_full(y, x, wd))

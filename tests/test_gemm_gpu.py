@@ -195,7 +195,8 @@ def test_deterministic_across_calls():
 @pytest.mark.parametrize("case", [
     ("int4", 16, 12288, 4096),  # decode kernel with a K split across workgroups
     ("int4", 256, 4096, 4096),  # MFMA kernel with a K split (fewer tiles than CUs)
-    ("int4", 4096, 4096, 6144),  # MFMA kernel: whole rounds, then the K-split tail launch
+    ("int4", 4096, 4096, 6144),  # MFMA kernel: whole rounds, then the tail as 128-row halves
+    ("fp8", 2048, 5120, 34816),  # fp8 W8A16 tall tiles: whole rounds, then the K-split tail launch
     ("w8a8", 16, 5120, 5120),  # per-token quantizer, then the W8A8 decode kernel
 ])
 def test_gemm_graph_replays_match_eager(case):
@@ -211,6 +212,10 @@ def test_gemm_graph_replays_match_eager(case):
         s = (np.abs(rng.standard_normal((n, k // 128))) * 0.02 + 1e-3).astype(np.float16)
         w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), to_dev(s), 1, 128)
         run = lambda: ops.gemm_int4_marlin_cuda(xd, w, sc, n, 1, 128)  # noqa: E731
+    elif fmt == "fp8":
+        codes, s = fp8_case(n, k, 128, 128, seed=63)
+        w, sc = _repack_fp8(codes, s, 128, 128)
+        run = lambda: ops.gemm_fp8_marlin_cuda(xd, w, sc, n, 128, 128)  # noqa: E731
     else:
         codes, s = fp8_case(n, k, 128, 128, seed=62)
         w, sc = _repack_fp8(codes, s, 128, 128)
@@ -309,8 +314,11 @@ def _check_full(y, x, wd):
 
 
 @pytest.mark.parametrize("shape", [(4096, 6144), (4096, 4096), (4096, 24576), (12288, 4096)])
-@pytest.mark.parametrize("m", [16, 4096])
+@pytest.mark.parametrize("m", [16, 1024, 4096])
 def test_full_size_against_gpu_fp32(shape, m):
+    """Configs 2 and 3 at full size, every row: M=16 on the decode kernels, M=1024 and
+    M=4096 on the MFMA kernel (gate_up at M=1024 and qkv at M=4096 end with the 128-row
+    halves launch)."""
     k, n = shape
     x, packed, s = _full_case(m, k, n, seed=k ^ n ^ m)
     w, sc = ops.repack_int4_marlin_cuda(packed, s, 1, 128)

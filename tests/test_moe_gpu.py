@@ -160,3 +160,44 @@ def test_routed_experts_graph_replays_match_eager():
         assert torch.equal(again, eager)
     ref = O.routed_experts_ref(h, experts, weights, gu[2], dn[2])
     assert_moe_close(out, ref, "moe graph t=1024")
+
+
+@pytest.mark.parametrize("t,e,hidden,inter,top_k", [(40, 8, 256, 128, 2), (1100, 16, 128, 128, 8)])
+def test_routed_experts_drops_out_of_range_experts(t, e, hidden, inter, top_k):
+    """Expert ids outside [0, n_experts) (-1 padding, ids >= n_experts) contribute nothing
+    and are not counted in the offsets; the block stays in bounds. The first case sorts in
+    one workgroup, the second (8800 rows) on the multi-kernel sort with a two-level plan.
+    The reference's index_add_ would raise on such ids; dropping them is this build's rule."""
+    g = 128
+    h, experts, weights, gu, dn = _moe_case(t, e, hidden, inter, top_k, g, seed=t + 3)
+    rng = np.random.default_rng(t)
+    bad = rng.random(experts.shape) < 0.15
+    bad[0, :] = True  # one token with no valid assignment: its output row is zero
+    junk = rng.choice(np.array([-1, -7, e, e + 5, 1 << 20], dtype=np.int64), size=experts.shape)
+    routed = np.where(bad, junk, experts)
+    print(f"dropped {int(bad.sum())} of {bad.size} assignments", flush=True)
+    out, offsets = ops.routed_experts_int4_cuda(to_dev(h, torch.bfloat16), to_dev(routed.astype(np.int32)),
+                                                to_dev(weights), gu[:2], dn[:2], inter, g)
+    counts = np.bincount(experts[~bad], minlength=e)
+    assert np.array_equal(offsets.cpu().numpy(), np.cumsum(counts).astype(np.int32))
+    # Oracle: the dropped assignments go to expert 0 with weight 0, so they add exact zeros.
+    ref = O.routed_experts_ref(h, np.where(bad, 0, experts), np.where(bad, 0.0, weights).astype(np.float32),
+                               gu[2], dn[2])
+    got = to_np(out)
+    assert np.all(got[0] == 0)
+    assert_moe_close(out, ref, f"moe with dropped experts t={t}")
+
+
+def test_grouped_gemm_clamps_offsets_to_rows():
+    """Offsets past `rows` are clamped (the last expert ends at row `rows`), and a
+    decreasing offset gives that expert no rows, so tiles never leave [0, rows)."""
+    e, n, k, g = 3, 64, 256, 128
+    w, s, deq = _experts(e, n, k, g, seed=21)
+    rows = 22
+    x = O.bf16_round(np.random.default_rng(5).standard_normal((rows, k)).astype(np.float32))
+    y = ops.grouped_gemm_int4_cuda(to_dev(x, torch.bfloat16), w, s, to_dev(np.array([5, 15, 40], np.int32)), n, g)
+    ref = np.concatenate([O.gemm_ref(x[:5], deq[0], None), O.gemm_ref(x[5:15], deq[1], None),
+                          O.gemm_ref(x[15:], deq[2], None)])
+    assert_close(y, ref, "offsets past rows")
+    y2 = ops.grouped_gemm_int4_cuda(to_dev(x, torch.bfloat16), w, s, to_dev(np.array([5, 3, 3], np.int32)), n, g)
+    assert_close(y2[:5], O.gemm_ref(x[:5], deq[0], None), "decreasing offsets")

@@ -362,3 +362,167 @@ def test_dequant_plain_int4_every_nibble(dtype):
     exp = torch.from_numpy(scale).repeat_interleave(16, 1)
     ref = (torch.from_numpy(q).float() * exp).to(tdt).float().numpy()
     assert np.array_equal(got, ref)
+
+
+# ---------------------------------------------------------------- W8A8 pins
+
+
+def _torch_quantize_rows(x, recip=False, clamp=1e-12, div=448.0, rounding="rne"):
+    """The block quantizer of test_qwen3_5.cpp:301-311 (fp32 amax, clamp_min(1e-12),
+    / 448, fp32 divide, float8_e4m3fn cast) applied per row by torch on the CPU.
+    The keyword arguments build plausible mistakes, which the pins must reject."""
+    xt = torch.from_numpy(np.ascontiguousarray(x)).float()
+    scale = xt.abs().amax(1, keepdim=True).clamp_min(clamp) / div
+    q = xt * (1.0 / scale) if recip else xt / scale
+    if rounding == "trunc":  # round toward zero onto the e4m3 grid
+        c = q.to(torch.float8_e4m3fn)
+        over = c.float().abs() > q.abs()
+        c = torch.where(over, (c.view(torch.uint8) - 1).view(torch.float8_e4m3fn), c)
+        return c.view(torch.uint8).numpy(), scale[:, 0].numpy()
+    return q.to(torch.float8_e4m3fn).view(torch.uint8).numpy(), scale[:, 0].numpy()
+
+
+def _quantizer_rows():
+    rng = np.random.default_rng(11)
+    k = 512
+    rows = [O.bf16_round(rng.standard_normal((6, k)).astype(np.float32) * 3)]
+    rows.append(np.zeros((1, k), np.float32))                                   # zero row: scale = 1e-12/448
+    tiny = O.bf16_round(rng.standard_normal((1, k)).astype(np.float32) * 1e-13)  # amax below the clamp
+    rows.append(tiny)
+    huge = O.bf16_round(rng.standard_normal((1, k)).astype(np.float32) * 1e37)
+    rows.append(huge)
+    # amax = 448 * 2^-3 makes the scale exactly 2^-3, so x / scale is exact and the
+    # e4m3 midpoints below are exact ties (RNE must pick the even code).
+    mids = (O.e4m3_decode(np.arange(1, 0x7E, dtype=np.uint8)) + O.e4m3_decode(np.arange(2, 0x7F, dtype=np.uint8))) / 2
+    ties = np.zeros((1, k), np.float32)
+    ties[0, 0] = 56.0
+    t = O.bf16_round((mids * 0.125).astype(np.float32))
+    t = t[O.bf16_round(t) == mids * 0.125][: k - 1]
+    ties[0, 1:1 + t.size] = t * np.where(np.arange(t.size) % 2, -1, 1)
+    rows.append(ties)
+    # Every non-negative bf16 value up to amax = 3.1875: some quotients x / scale
+    # round differently from x * (1 / scale) (found by the same search on the CPU).
+    bits = (np.arange(0, 0x4060, dtype=np.uint32) << 16).view(np.float32)
+    allv = np.concatenate([[np.float32(3.1875)], bits[bits <= 3.1875]]).astype(np.float32)
+    rows.append(allv[None, :])
+    width = max(r.shape[1] for r in rows)
+    return [np.pad(r, ((0, 0), (0, width - r.shape[1]))) for r in rows]
+
+
+def test_quantize_per_token_matches_reference_quantizer():
+    for x in _quantizer_rows():
+        codes, scale = O.quantize_per_token_e4m3(x)
+        ref_c, ref_s = _torch_quantize_rows(x)
+        assert np.array_equal(scale.view(np.uint32), ref_s.view(np.uint32))
+        assert np.array_equal(codes, ref_c)
+
+
+@pytest.mark.parametrize("mutant", [dict(recip=True), dict(clamp=1e-6), dict(div=447.0), dict(rounding="trunc")])
+def test_quantizer_pin_rejects_mutants(mutant):
+    """Each plausible mistake (x * (1/scale), another clamp, another divisor, truncation)
+    disagrees with the reference quantizer on these rows, so the pin above resolves it."""
+    differs = False
+    for x in _quantizer_rows():
+        c, s = _torch_quantize_rows(x, **mutant)
+        ref_c, ref_s = _torch_quantize_rows(x)
+        differs |= not (np.array_equal(c, ref_c) and np.array_equal(s, ref_s))
+    assert differs
+
+
+@pytest.mark.parametrize("block_n,group", [(128, 128), (1, 128), (16, 256)])
+def test_gemm_w8a8_ref_matches_torch_float64(block_n, group):
+    rng = np.random.default_rng(12)
+    m, n, k = 9, 200, 512
+    x = O.bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    cx, sx = O.quantize_per_token_e4m3(x)
+    w = O.bf16_round(rng.standard_normal((n, k)).astype(np.float32) * 0.02)
+    cw, sw = O.fp8_block_quantize(w, block_n, group) if block_n == group else (
+        O.e4m3_encode(w * 64), (rng.random((-(-n // block_n), k // group)) * 0.02 + 1e-3).astype(np.float32))
+    got = O.gemm_w8a8_ref(cx, sx, cw, sw, block_n, group, dtype=None)
+    xt = torch.from_numpy(cx).view(torch.float8_e4m3fn).double() * torch.from_numpy(sx).double()[:, None]
+    st = torch.from_numpy(np.asarray(sw, np.float32)).double().repeat_interleave(block_n, 0)[:n].repeat_interleave(group, 1)
+    wt = torch.from_numpy(cw).view(torch.float8_e4m3fn).double() * st
+    ref = (xt @ wt.T).float().numpy()
+    assert np.allclose(got, ref, rtol=1e-6, atol=1e-6)
+    # A transposed scale expansion or a dropped row scale would not match.
+    assert not np.allclose(got, (xt @ wt.T / torch.from_numpy(sx).double()[:, None]).float().numpy(), rtol=1e-3)
+    bf = O.gemm_w8a8_ref(cx, sx, cw, sw, block_n, group)
+    assert np.array_equal(bf, O.bf16_round(got))
+
+
+# ---------------------------------------------------------------- MoE pins
+
+
+def _routed_experts_torch(h, top_experts, top_weights, gate_up, down, round_silu=True, round_weight=True):
+    """routed_experts (paged_forward.cpp:116-129) step by step with torch on the CPU,
+    at::_grouped_mm included, in the activation dtype. round_silu / round_weight = False
+    drop one rounding point each (plausible mistakes the pins must reject)."""
+    n_experts = gate_up.shape[0]
+    top_k = top_experts.shape[-1]
+    assigned = top_experts.flatten()
+    order = torch.argsort(assigned, stable=True)
+    tokens = torch.floor_divide(order, top_k)
+    counts = torch.zeros(n_experts, dtype=torch.int32).index_add_(
+        0, assigned.index_select(0, order), torch.ones_like(order, dtype=torch.int32))
+    offsets = torch.cumsum(counts, 0, dtype=torch.int32)
+    rows = h.index_select(0, tokens)
+    gu = torch._grouped_mm(rows, gate_up.transpose(1, 2), offsets)
+    g, u = gu.chunk(2, -1)
+    if round_silu:
+        act = torch.nn.functional.silu(g) * u
+    else:
+        act = (torch.nn.functional.silu(g.float()) * u.float()).to(h.dtype)
+    d = torch._grouped_mm(act, down.transpose(1, 2), offsets)
+    w = top_weights.flatten().index_select(0, order).unsqueeze(1)
+    weighted = d * w.to(d.dtype) if round_weight else (d.float() * w).to(d.dtype)
+    out = torch.zeros_like(h).index_add_(0, tokens, weighted)
+    return out, dict(order=order, offsets=offsets, gate_up=gu, act=act, down=d, weighted=weighted)
+
+
+def _moe_case(seed=13, e=16, h_dim=128, inter=64, t=96, top_k=4):
+    rng = np.random.default_rng(seed)
+    h = O.bf16_round(rng.standard_normal((t, h_dim)).astype(np.float32))
+    gate_up = O.bf16_round(rng.standard_normal((e, 2 * inter, h_dim)).astype(np.float32) * 0.1)
+    down = O.bf16_round(rng.standard_normal((e, h_dim, inter)).astype(np.float32) * 0.1)
+    experts, weights = O.zipf_routing(t, e, top_k, seed=seed)
+    experts[0, 0], experts[1, 0] = experts[1, 0], experts[0, 0]  # keep an unsorted start
+    bf = torch.bfloat16
+    tin = (torch.from_numpy(h).to(bf), torch.from_numpy(experts), torch.from_numpy(weights),
+           torch.from_numpy(gate_up).to(bf), torch.from_numpy(down).to(bf))
+    return (h, experts, weights, gate_up, down), tin
+
+
+def _bits_equal_frac(a, b):
+    a = O.bf16_bits(np.asarray(a, np.float32))
+    b = O.bf16_bits(np.asarray(b, np.float32))
+    return float(np.mean(a == b)), int(np.max(np.abs(a.astype(np.int64) - b.astype(np.int64))))
+
+
+def test_routed_experts_stages_match_reference_steps():
+    """Each rounding point of the oracle against the reference's steps run by torch:
+    sort and offsets exactly; the grouped GEMM outputs, silu(g)*u and the weighted
+    terms bit for bit except where float64 and fp32 accumulation round apart (at most
+    one bf16 ulp, in a small fraction); the index_add_ sum within the MoE tolerance."""
+    args, tin = _moe_case()
+    out, parts = O.routed_experts_ref(*args, parts=True)
+    ref_out, ref = _routed_experts_torch(*tin)
+    assert np.array_equal(parts["order"], ref["order"].numpy())
+    assert np.array_equal(parts["offsets"], ref["offsets"].numpy())
+    for name in ("gate_up", "act", "down", "weighted"):
+        frac, ulps = _bits_equal_frac(parts[name], ref[name].float().numpy())
+        assert frac >= 0.99 and ulps <= 1, (name, frac, ulps)
+    r = ref_out.float().numpy()
+    rel = np.linalg.norm(out - r) / np.linalg.norm(r)
+    assert rel <= 5e-3 and np.abs(out - r).max() / np.abs(r).max() < 5e-2
+
+
+@pytest.mark.parametrize("mutant", [dict(round_silu=False), dict(round_weight=False)])
+def test_routed_experts_pin_rejects_dropped_rounding(mutant):
+    """With a rounding point dropped, the reference's steps no longer match the
+    oracle's stages at the bit level the pin above demands."""
+    args, tin = _moe_case()
+    _, parts = O.routed_experts_ref(*args, parts=True)
+    _, mut = _routed_experts_torch(*tin, **mutant)
+    stage = "act" if "round_silu" in mutant else "weighted"
+    frac, _ = _bits_equal_frac(parts[stage], mut[stage].float().numpy())
+    assert frac < 0.99, frac

@@ -1,5 +1,5 @@
 """Parity of the non-repacked int4 GEMM (plm_gemm_int4_plain; gemm_int4_cuda and
-gemm_int4_split_cuda of pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:269-297) with the CPU
+gemm_int4_split_cuda of pulsarlm-core/inc/pulsarlm/kernels/ops.hpp:272-297) with the CPU
 oracle: W = round(fp32(q * scale)) (int4_gemm.cu:136-138). The reference has no test of
 its own for these ops; the checks follow test_marlin.cpp's: identity-GEMM exactness and
 the dequantize-then-matmul tolerance (elementwise 2e-2 + 2e-2 |ref|, rel-L2 <= 5e-3), plus
