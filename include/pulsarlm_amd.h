@@ -9,10 +9,12 @@
  *
  * Weight layout ("plm tile layout", opaque to callers): the N x K weight is cut
  * into 16-row x 128-column tiles, strip-major (all K tiles of rows 0..15, then
- * rows 16..31, ...). An int4 tile is 1 KiB: 64 lanes x 16 bytes, lane
- * (n % 16) + 16 * ((k % 32) / 8) holding, in its four 32-bit words t = (k % 128)
- * / 32, the 8 consecutive K values k % 8 of its column as offset-binary nibbles
- * (q + 8), even k in nibbles 0-3 and odd k in nibbles 4-7. An fp8 tile is 2 KiB:
+ * rows 16..31, ...). An int4 tile is 1 KiB: 64 lanes x 16 bytes. Lane
+ * 16 g + 4 c + i holds in its 32-bit word t = (k % 128) / 32 the offset-binary
+ * nibbles (q + 8) of rows 4 c + r (r = 0..3) at K = 32 t + 8 g + 4 h + i (h = 0, 1),
+ * (r, h) in nibble 4 (r % 2) + 2 h + r / 2: four rows by two K values, the operand
+ * of the matrix-core dequant (see plm_common.hpp). An fp8 tile is 2 KiB, lane
+ * (n % 16) + 16 * ((k % 32) / 8) holding the 8 consecutive K bytes k % 8 of its row:
  * two such 1 KiB halves (t / 2), each lane holding 8 bytes per t. Padding rows
  * and columns hold q = 0. Scales are stored in their source dtype as
  * [N/16 strips][ceil(K_pad / group_size) groups][16 or 1], one per column, or

@@ -499,7 +499,7 @@ def zipf_routing(tokens: int, n_experts: int, top_k: int, alpha: float = 1.2, se
 
 
 def _plm_coords(n: int, k: int):
-    """For every (row, col) of an N x K matrix: strip, k tile, step t, lane, i."""
+    """For every (row, col) of an N x K fp8 matrix: strip, k tile, step t, lane, i."""
     rows = np.arange(n)[:, None]
     cols = np.arange(k)[None, :]
     strip = rows // 16
@@ -510,17 +510,31 @@ def _plm_coords(n: int, k: int):
     return strip, kt, t, lane, i
 
 
+def _plm_int4_coords(n: int, k: int):
+    """For every (row, col) of an N x K int4 matrix: word index and nibble position.
+    Word ((strip*KT + kt)*64 + lane)*4 + t with lane = 16 g + 4 c + i holds column
+    strip*16 + 4c + r at K = kt*128 + 32t + 8g + 4h + i in nibble 4 (r % 2) + 2h + r // 2."""
+    rows = np.arange(n)[:, None]
+    cols = np.arange(k)[None, :]
+    strip, kt, t = rows // 16, cols // 128, (cols % 128) // 32
+    kk = cols % 32
+    g, h, i = kk // 8, (kk % 8) // 4, kk % 4
+    c, r = (rows % 16) // 4, rows % 4
+    lane = 16 * g + 4 * c + i
+    pos = 4 * (r % 2) + 2 * h + r // 2
+    ktiles = -(-k // 128)
+    widx = ((strip * ktiles + kt) * 64 + lane) * 4 + t
+    return np.broadcast_to(widx, (n, k)), np.broadcast_to(pos, (n, k))
+
+
 def plm_layout_int4(packed) -> np.ndarray:
     """int32 [N, K/8] -> plm int4 layout as uint32 words (padding nibbles = 8, i.e. q = 0)."""
     q = unpack_int4(packed).astype(np.int64)
     n, k = q.shape
     strips, ktiles = -(-n // 16), -(-k // 128)
-    words = np.zeros(strips * ktiles * 256, dtype=np.uint64)
-    # Start from all-padding words, then clear and set each real nibble.
+    # Start from all-padding words, then set each real nibble.
     nib_all = np.full((strips * ktiles * 256, 8), 8, dtype=np.uint64)
-    strip, kt, t, lane, i = _plm_coords(n, k)
-    widx = ((strip * ktiles + kt) * 64 + lane) * 4 + t
-    pos = np.broadcast_to(np.where(i % 2 == 1, 4 + i // 2, i // 2), widx.shape)
+    widx, pos = _plm_int4_coords(n, k)
     nib_all[widx.reshape(-1), pos.reshape(-1)] = ((q & 0xF) ^ 8).reshape(-1).astype(np.uint64)
     words = (nib_all << (np.arange(8, dtype=np.uint64) * 4)).sum(axis=1)
     return (words & 0xFFFFFFFF).astype(np.uint32)

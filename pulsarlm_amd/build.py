@@ -45,10 +45,14 @@ SOURCE_FLAGS = {"gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 def _compile(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
-    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
+    # The compiler's per-kernel resource report (registers, LDS, scratch) is kept next to
+    # the object: tests/test_build.py checks that no kernel spills to scratch.
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-Rpass-analysis=kernel-resource-usage", "-c",
+           str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")
+    (BUILD / (Path(src).stem + ".resources.txt")).write_text(res.stderr)
     return obj
 
 

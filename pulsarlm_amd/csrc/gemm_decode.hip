@@ -490,10 +490,18 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
             constexpr int kLoads = CH * SG * NL;
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");
         }
-        // int4: every tile's x fragments and scale constants of this batch are read and set
-        // up before the first dequant, i.e. while the weight loads are still in flight.
+        // int4: every tile's x fragments and (for up to four tiles x strips) scale constants
+        // of this batch are read and set up before the first dequant, i.e. while the weight
+        // loads are still in flight. Larger batches set the scales up per tile (registers).
+        constexpr bool kScalesAhead = CH * SG <= 4;
+        auto int4_scale_of = [&](int i, int sj) {
+            const uint8_t* sp = ss + (((sj << a.nkt_shift) + i) * EB) + (SC == 2 ? 0 : col16 * (WIDE ? 4 : 2));
+            const uint32_t bits = WIDE ? *reinterpret_cast<const uint32_t*>(sp)
+                                       : static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(sp));
+            return make_int4_scale<BF16>(scale_from_bits<WIDE>(bits, bf16_scale));
+        };
         [[maybe_unused]] u32x4_t xfb[CH][4];
-        [[maybe_unused]] int4_scale k4b[CH][SG];
+        [[maybe_unused]] int4_scale k4b[kScalesAhead ? CH : 1][kScalesAhead ? SG : 1];
         if constexpr (F == PLM_INT4 && !A8) {
 #pragma unroll
             for (int ii = 0; ii < CH; ++ii) {
@@ -501,12 +509,9 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
                 const uint8_t* xp = xs + (((xrow << a.nkt_shift) + i) << 8) + kq * 16;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) xfb[ii][t] = *reinterpret_cast<const u32x4_t*>(xp + 64 * t);
+                if constexpr (kScalesAhead) {
 #pragma unroll
-                for (int sj = 0; sj < SG; ++sj) {
-                    const uint8_t* sp = ss + (((sj << a.nkt_shift) + i) * EB) + (SC == 2 ? 0 : col16 * (WIDE ? 4 : 2));
-                    const uint32_t bits = WIDE ? *reinterpret_cast<const uint32_t*>(sp)
-                                               : static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(sp));
-                    k4b[ii][sj] = make_int4_scale<BF16>(scale_from_bits<WIDE>(bits, bf16_scale));
+                    for (int sj = 0; sj < SG; ++sj) k4b[ii][sj] = int4_scale_of(i, sj);
                 }
             }
         }
@@ -516,10 +521,14 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
             if (i >= nkt_w) break;  // wave-uniform
             if constexpr (F == PLM_INT4 && !A8) {
 #pragma unroll
-                for (int sj = 0; sj < SG; ++sj)
+                for (int sj = 0; sj < SG; ++sj) {
+                    int4_scale k4;
+                    if constexpr (kScalesAhead) k4 = k4b[ii][sj];
+                    else k4 = int4_scale_of(i, sj);
 #pragma unroll
                     for (int t = 0; t < 4; ++t)
-                        acc[sj] = mfma16x16x32<BF16>(xfb[ii][t], dq_int4<BF16>(wv[ii][sj][0][t], k4b[ii][sj]), acc[sj]);
+                        acc[sj] = mfma16x16x32<BF16>(xfb[ii][t], dq_int4<BF16>(wv[ii][sj][0][t], k4), acc[sj]);
+                }
                 continue;
             }
             if constexpr (A8) {
@@ -640,6 +649,7 @@ decode_config choose_decode(plm_format f, int64_t m, int64_t n, int64_t k) {
         }
     }
     if (c.sp == 4 && (c.tpw != 1 || c.nw != 16)) c.sp = 2;  // four strips: one instantiation only
+    if (c.sp > 1) c.tpw = 1;                                 // two tiles per batch: one strip only
     (void)f;
     c.strip_groups = static_cast<int>(ceil_div(strips, c.sp));
     // Split K across workgroups only when the column blocks alone cannot fill the GPU.
@@ -708,10 +718,18 @@ void launch_decode_nw(const decode_args& a, const decode_config& c, bool uniform
     }
 }
 
+// Two tiles per batch only with one strip and one row block: the other combinations hold
+// too many fragments for the 128 VGPRs of 1024-thread workgroups (they spilled) and were
+// never the measured choice.
 template <plm_format F, bool BF16, int SP, int RB>
 void launch_decode_sp(const decode_args& a, const decode_config& c, bool uniform, hipStream_t s) {
-    if (c.tpw == 1) launch_decode_nw<F, BF16, SP, 1, RB>(a, c, uniform, s);
-    else launch_decode_nw<F, BF16, SP, 2, RB>(a, c, uniform, s);
+    if constexpr (SP == 1 && RB == 1) {
+        if (c.tpw == 2) {
+            launch_decode_nw<F, BF16, SP, 2, RB>(a, c, uniform, s);
+            return;
+        }
+    }
+    launch_decode_nw<F, BF16, SP, 1, RB>(a, c, uniform, s);
 }
 
 template <plm_format F, bool BF16, int RB = 1>

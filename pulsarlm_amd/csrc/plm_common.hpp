@@ -153,53 +153,102 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
 }
 
 // ---------------------------------------------------------------------------
-// Exact in-register dequantization to the MFMA operand: round(q * round(s)),
-// the value the reference's kernels feed their MMAs (pulsarlm-core/src/kernels/
-// marlin.cu:78-84,123-151,180-194).
+// Exact dequantization to the MFMA operand: round(q * round(s)), the value the
+// reference's kernels feed their MMAs (pulsarlm-core/src/kernels/marlin.cu:78-84,
+// 123-151,180-194).
 //
-// int4: a plm word holds K pair p = (2p, 2p+1) in nibbles p and p + 4 as u = q + 8.
-// One v_bitop3 turns two nibbles at bits 0-3 of each 16-bit half into the fp16
-// pair (1024 + u, 1024 + u'), or at bits 4-7 into (1024 + 16u, ...). v_fma_mix_f32
-// then computes (1024 + u) * s - 1032 s, resp. (1024 + 16u) * s/16 - 72 s, which
-// equals q * s with no rounding (every product and sum fits fp32's 24 bits), and
-// v_cvt_pk_{bf16,f16}_f32 rounds the pair once, to nearest even.
+// int4 runs on the matrix core. A lane's plm word holds 8 nibbles u = q + 8 of four
+// columns and two K quads: lane l = 16 g + 4 c + i, nibble p holds column
+// 4 c + r and K 8 g + 4 h + i of its 32-wide K slice, with r = 2 (p % 2) + p / 4 and
+// h = (p % 4) / 2. v_bitop3 turns the nibbles into 16-bit floats a = base + u (exact),
+// two per dword, and v_mfma_f32_4x4x4_16b (16 independent 4 x 4 x 4 products) with a
+// diagonal B operand (block b: B[j][j] = s of column 4 (b % 4) + j) and C = -(base + 8) s
+// gives D[i][j] = (base + u) s - (base + 8) s = q s exactly: every product fits fp32's
+// 24 bits and the sum is exactly representable. Block b's D lands in lane 4 b + j,
+// register i: column l % 16, K 8 g + 4 h + i -- the lane's B fragment of
+// v_mfma_f32_16x16x32 (column l % 16, K 8 (l / 16) + 0..7) for h = 0, 1, with no
+// shuffle. One v_cvt_pk per pair rounds once, to nearest even. Per word: 4 bitop3
+// (+3 shifts for bf16, +1 for fp16), 2 small MFMAs and 4 converts, against 17 VALU ops
+// for the same 8 weights per lane with v_fma_mix.
+//   bf16: a = 128 + u (0x4300 | u); all four registers use nibbles at bits 0-3 of a
+//         16-bit half, so three of the four dwords take a shift.
+//   fp16: registers 0-1 take nibbles at bits 0-3 as 1024 + u (0x6400 | u), registers
+//         2-3 nibbles at bits 4-7 as 64 + u (exponent 6: 0x5400 | u << 4), so one
+//         shift (by 8) serves all four dwords; C = -(1032 or 72) s per register.
+// The B diagonal and C are per lane (lane l's own column scale at register l % 4).
+// Domain: (128 + u) s must stay finite, so bf16-rounded scales must be below 2^120 in
+// magnitude (fp16 ones always are); plm_dequant has no such limit.
 // ---------------------------------------------------------------------------
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4_t;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+
 struct int4_scale {
-    float s0, c0;  // nibbles at bits 0-3:  s, -1032 s
-    float s1, c1;  // nibbles at bits 4-7:  s / 16, -72 s
+    u32x2_t diag;  // B operand of the 4x4x4 MFMA: the lane's scale at register lane % 4
+    float c;       // -(base + 8) * s for the lane's register lane % 4
 };
 
 template <bool BF16> __device__ __forceinline__ int4_scale make_int4_scale(float raw) {
-    const float s = round_to<BF16>(raw);
-    return {s, -1032.f * s, s * 0.0625f, -72.f * s};
+    const int j = __lane_id() & 3;
+    int4_scale k;
+    uint32_t bits;
+    float s;
+    if constexpr (BF16) {
+        s = round_bf16(raw);
+        bits = f32_to_bf16_bits(s);
+        k.c = -136.f * s;
+    } else {
+        s = round_f16(raw);
+        bits = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(s)));
+        k.c = (j < 2 ? -1032.f : -72.f) * s;
+    }
+    const uint32_t sh = (j & 1) ? bits << 16 : bits;
+    k.diag[0] = j < 2 ? sh : 0u;
+    k.diag[1] = j < 2 ? 0u : sh;
+    return k;
 }
 
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
     return __builtin_amdgcn_bitop3_b32(a, mask, bits, 0xEA);  // (a & mask) | bits
 }
 
-__device__ __forceinline__ float half_lo(uint32_t h) {
-    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
-    return static_cast<float>(__builtin_bit_cast(f16x2_t, h)[0]);
-}
-__device__ __forceinline__ float half_hi(uint32_t h) {
-    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
-    return static_cast<float>(__builtin_bit_cast(f16x2_t, h)[1]);
+template <bool BF16> __device__ __forceinline__ f32x4_t mfma4x4x4(u32x2_t a, u32x2_t b, f32x4_t c) {
+    if constexpr (BF16) {
+        return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b), c,
+                                                      0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c, 0,
+                                                  0, 0);
+    }
 }
 
 template <bool BF16> __device__ __forceinline__ u32x4_t dq_int4(uint32_t w, const int4_scale& k) {
-    const uint32_t h0 = and_or(w, 0x000F000Fu, 0x64006400u);  // K0, K1
-    const uint32_t h1 = and_or(w, 0x00F000F0u, 0x64006400u);  // K2, K3 (x16)
-    const uint32_t w8 = w >> 8;
-    const uint32_t h2 = and_or(w8, 0x000F000Fu, 0x64006400u);  // K4, K5
-    const uint32_t h3 = and_or(w8, 0x00F000F0u, 0x64006400u);  // K6, K7 (x16)
+    u32x2_t a0, a1;
+    if constexpr (BF16) {
+        a0[0] = and_or(w, 0x000F000Fu, 0x43004300u);
+        a0[1] = and_or(w >> 4, 0x000F000Fu, 0x43004300u);
+        a1[0] = and_or(w >> 8, 0x000F000Fu, 0x43004300u);
+        a1[1] = and_or(w >> 12, 0x000F000Fu, 0x43004300u);
+    } else {
+        const uint32_t w8 = w >> 8;
+        a0[0] = and_or(w, 0x000F000Fu, 0x64006400u);
+        a0[1] = and_or(w, 0x00F000F0u, 0x54005400u);
+        a1[0] = and_or(w8, 0x000F000Fu, 0x64006400u);
+        a1[1] = and_or(w8, 0x00F000F0u, 0x54005400u);
+    }
+    const f32x4_t c = {k.c, k.c, k.c, k.c};
+    const f32x4_t d0 = mfma4x4x4<BF16>(a0, k.diag, c);
+    const f32x4_t d1 = mfma4x4x4<BF16>(a1, k.diag, c);
     u32x4_t b;
-    b[0] = pack2<BF16>(__builtin_fmaf(half_lo(h0), k.s0, k.c0), __builtin_fmaf(half_hi(h0), k.s0, k.c0));
-    b[1] = pack2<BF16>(__builtin_fmaf(half_lo(h1), k.s1, k.c1), __builtin_fmaf(half_hi(h1), k.s1, k.c1));
-    b[2] = pack2<BF16>(__builtin_fmaf(half_lo(h2), k.s0, k.c0), __builtin_fmaf(half_hi(h2), k.s0, k.c0));
-    b[3] = pack2<BF16>(__builtin_fmaf(half_lo(h3), k.s1, k.c1), __builtin_fmaf(half_hi(h3), k.s1, k.c1));
+    b[0] = pack2<BF16>(d0[0], d0[1]);
+    b[1] = pack2<BF16>(d0[2], d0[3]);
+    b[2] = pack2<BF16>(d1[0], d1[1]);
+    b[3] = pack2<BF16>(d1[2], d1[3]);
     return b;
 }
+
+// Nibble position of (column c16 % 4, K quad h) in a plm int4 word (see above).
+__host__ __device__ constexpr int int4_nibble_pos(int r, int h) { return 4 * (r & 1) + 2 * h + (r >> 1); }
 
 // fp8: v_cvt_pk_f32_fp8 decodes two e4m3 bytes exactly; the product with the
 // rounded scale is exact in fp32 (4 x 11 significant bits) and rounded once.

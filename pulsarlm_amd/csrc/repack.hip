@@ -44,21 +44,11 @@ int cu_count() {
 
 namespace {
 
-// Source word (8 nibbles, LSB first, two's complement) -> plm word: offset
-// binary, even K in nibbles 0-3 and odd K in nibbles 4-7.
-__device__ __forceinline__ uint32_t plm_word_from_lsb_first(uint32_t src) {
-    uint32_t out = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t nib = ((src >> (4 * i)) & 0xfu) ^ 8u;
-        const int pos = (i & 1) ? 4 + (i >> 1) : (i >> 1);
-        out |= nib << (4 * pos);
-    }
-    return out;
-}
-
-// One thread per 32-bit word of the int4 layout: word ((strip*KT + kt)*64 + lane)*4 + t
-// holds column strip*16 + lane%16, K = kt*128 + 32t + 8*(lane/16) + 0..7.
+// One thread per 32-bit word of the int4 layout: word ((strip*KT + kt)*64 + lane)*4 + t,
+// lane = 16 g + 4 c + i, holds in nibble int4_nibble_pos(r, h) the value q + 8 of column
+// strip*16 + 4c + r at K = kt*128 + 32t + 8g + 4h + i (r, h in 0..3 x 0..1). The eight
+// values come from one source int32 (K/8 index kt*16 + 4t + g, nibble 4h + i) of each of
+// the four columns.
 __global__ void repack_int4_kernel(const int32_t* __restrict__ src, uint32_t* __restrict__ dst, int64_t n,
                                    int64_t k, int64_t ktiles, int64_t total) {
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -68,10 +58,19 @@ __global__ void repack_int4_kernel(const int32_t* __restrict__ src, uint32_t* __
     const int64_t tile = idx >> 8;
     const int64_t kt = tile % ktiles;
     const int64_t strip = tile / ktiles;
-    const int64_t col = strip * kTileN + (lane & 15);
-    const int64_t k0 = kt * kTileK + 32 * t + 8 * (lane >> 4);
-    uint32_t word = 0x88888888u;  // q = 0
-    if (col < n && k0 < k) word = plm_word_from_lsb_first(static_cast<uint32_t>(src[col * (k / 8) + k0 / 8]));
+    const int g = lane >> 4, c = (lane >> 2) & 3, i = lane & 3;
+    const int64_t k8 = kt * kTileK + 32 * t + 8 * g;  // first K of the source word
+    uint32_t word = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t col = strip * kTileN + 4 * c + r;
+        const uint32_t sw = (col < n && k8 < k) ? static_cast<uint32_t>(src[col * (k / 8) + k8 / 8]) : 0u;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t nib = ((sw >> (4 * (4 * h + i))) & 0xfu) ^ 8u;  // padding: q = 0
+            word |= nib << (4 * int4_nibble_pos(r, h));
+        }
+    }
     dst[idx] = word;
 }
 
@@ -115,9 +114,9 @@ __global__ void repack_scale_kernel(const T* __restrict__ src, T* __restrict__ d
     dst[idx] = v;
 }
 
-// Reference Marlin words -> plm int4 words. Marlin word index
-// ((cb*KTm + k/32)*8 + subtile)*32 + lane_m with lane_m = 4*(n%8) + pair holds,
-// in nibble j + 4*odd, K offset 2*pair + odd + 8j (marlin.cu:86-117).
+// Reference Marlin words -> plm int4 words (the mapping of repack_int4_kernel). Marlin
+// word index ((cb*KTm + k/32)*8 + subtile)*32 + lane_m with lane_m = 4*(n%8) + pair holds,
+// in nibble j + 4*odd, K offset 2*pair + odd + 8j (marlin.cu:86-117), already as q ^ 8.
 __global__ void convert_marlin_int4_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, int64_t n,
                                            int64_t k, int64_t ktiles, int64_t total) {
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -127,23 +126,25 @@ __global__ void convert_marlin_int4_kernel(const uint32_t* __restrict__ src, uin
     const int64_t tile = idx >> 8;
     const int64_t kt = tile % ktiles;
     const int64_t strip = tile / ktiles;
-    const int64_t col = strip * kTileN + (lane & 15);
-    const int64_t k0 = kt * kTileK + 32 * t + 8 * (lane >> 4);
-    uint32_t word = 0x88888888u;
-    if (col < n && k0 < k) {
-        const int64_t ktm = ceil_div(k, 32);
-        const int64_t cb = col / 64, subtile = (col % 64) / 8;
-        word = 0;
+    const int g = lane >> 4, c = (lane >> 2) & 3, i = lane & 3;
+    const int64_t ktm = ceil_div(k, 32);
+    uint32_t word = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int64_t kk = k0 + i;
-            const int c = static_cast<int>(kk % 32);
-            const int pair = (c % 8) / 2, odd = c % 2, j = c / 8;
-            const int lane_m = static_cast<int>(col % 8) * 4 + pair;
-            const uint32_t w = src[((cb * ktm + kk / 32) * 8 + subtile) * 32 + lane_m];
-            const uint32_t nib = (w >> (4 * (j + 4 * odd))) & 0xfu;  // already q ^ 8
-            const int pos = (i & 1) ? 4 + (i >> 1) : (i >> 1);
-            word |= nib << (4 * pos);
+    for (int r = 0; r < 4; ++r) {
+        const int64_t col = strip * kTileN + 4 * c + r;
+        const int64_t cb = col / 64, subtile = (col % 64) / 8;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t kk = kt * kTileK + 32 * t + 8 * g + 4 * h + i;
+            uint32_t nib = 8u;  // padding: q = 0
+            if (col < n && kk < k) {
+                const int cm = static_cast<int>(kk % 32);
+                const int pair = (cm % 8) / 2, odd = cm % 2, j = cm / 8;
+                const int lane_m = static_cast<int>(col % 8) * 4 + pair;
+                const uint32_t w = src[((cb * ktm + kk / 32) * 8 + subtile) * 32 + lane_m];
+                nib = (w >> (4 * (j + 4 * odd))) & 0xfu;
+            }
+            word |= nib << (4 * int4_nibble_pos(r, h));
         }
     }
     dst[idx] = word;
@@ -212,8 +213,10 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ w, const void* __rest
     const int lane = static_cast<int>(row % kTileN) + 16 * kq;
     float q;
     if constexpr (F == PLM_INT4) {
-        const uint32_t word = reinterpret_cast<const uint32_t*>(w)[((strip * ktiles + kt) * 64 + lane) * 4 + t];
-        const int pos = (i & 1) ? 4 + (i >> 1) : (i >> 1);
+        const int c16 = static_cast<int>(row % kTileN);
+        const int lane4 = 16 * kq + 4 * (c16 >> 2) + (i & 3);
+        const uint32_t word = reinterpret_cast<const uint32_t*>(w)[((strip * ktiles + kt) * 64 + lane4) * 4 + t];
+        const int pos = int4_nibble_pos(c16 & 3, i >> 2);
         q = static_cast<float>(static_cast<int>((word >> (4 * pos)) & 0xfu) - 8);
     } else {
         const int64_t off = ((strip * ktiles + kt) * 2 + t / 2) * 1024 + lane * 16 + (t % 2) * 8 + i;

@@ -185,24 +185,75 @@ def test_marlin_round_trip(n, k):
 
 
 def test_plm_layout_int4_known_word():
-    """include/pulsarlm_amd.h: word ((strip*KT + kt)*64 + lane)*4 + t, lane = n%16 + 16*((k%32)/8),
-    even k in nibbles 0-3, odd k in nibbles 4-7, offset binary."""
+    """include/pulsarlm_amd.h: word ((strip*KT + kt)*64 + lane)*4 + t, lane = 16 g + 4 c + i,
+    nibble 4 (r % 2) + 2 h + r // 2 holds q + 8 of column strip*16 + 4c + r at
+    K = kt*128 + 32t + 8g + 4h + i. Derived by hand for one word."""
     n, k = 32, 256
     q = np.zeros((n, k), dtype=np.int64)
-    # column 17 (strip 1, col16 = 1), K 128 + 64 + 16 .. +7 -> kt 1, t 2, kq 2.
-    base = 128 + 64 + 16
-    vals = [1, -1, 2, -2, 3, -3, 7, -8]
-    q[17, base:base + 8] = vals
+    # strip 1, columns 24..27 (c = 2, r = 0..3); kt 1, t 2, g 1 (K 128 + 64 + 8 ..), i = 3.
+    vals = {(24, 0): 1, (25, 0): -1, (26, 0): 2, (27, 0): -2, (24, 1): 3, (25, 1): -3, (26, 1): 7, (27, 1): -8}
+    for (col, h), v in vals.items():
+        q[col, 128 + 64 + 8 + 4 * h + 3] = v
     words = O.plm_layout_int4(O.pack_int4(q))
-    ktiles = 2
-    lane = 1 + 16 * 2
-    w = int(words[((1 * ktiles + 1) * 64 + lane) * 4 + 2])
-    expect = 0
-    for i, v in enumerate(vals):
-        pos = 4 + i // 2 if i % 2 else i // 2
-        expect |= (v + 8) << (4 * pos)
-    assert w == expect
+    lane = 16 * 1 + 4 * 2 + 3
+    w = int(words[((1 * 2 + 1) * 64 + lane) * 4 + 2])
+    # nibble p: (r, h) = (0,0) (2,0) (0,1) (2,1) (1,0) (3,0) (1,1) (3,1)
+    order = [(24, 0), (26, 0), (24, 1), (26, 1), (25, 0), (27, 0), (25, 1), (27, 1)]
+    expect = sum((vals[c] + 8) << (4 * p) for p, c in enumerate(order))
+    assert w == expect == 0x0567FBA9  # nibbles p0..p7 = 9, A, B, F, 7, 6, 5, 0
     assert int(words[0]) == 0x88888888
+    assert np.count_nonzero(words != 0x88888888) == 1
+
+
+def _mfma4x4x4(a, b, c):
+    """v_mfma_f32_4x4x4_16b as measured on gfx950: 16 blocks b = lane // 4; A[i][k] of a
+    block in lane 4b + i, register k; B[k][j] in lane 4b + j, register k; D[i][j] (+ C)
+    in lane 4b + j, register i. a, b: [64, 4] values; c: [64, 4]."""
+    a = a.reshape(16, 4, 4)          # block, i, k
+    bt = b.reshape(16, 4, 4)         # block, j, k
+    d = np.einsum("bik,bjk->bji", a.astype(np.float64), bt.astype(np.float64))  # block, j, i
+    return d.reshape(64, 4) + c
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_plm_int4_matrix_core_dequant(dtype):
+    """The kernels' dequant, emulated bit for bit on the CPU: nibbles -> 16-bit floats by
+    and/or masks, two 4x4x4 products with the scale diagonal, converts. Each lane must end
+    up with the exact reference weights round(q * round(s)) of column lane % 16 at
+    K 8 (lane // 16) + 0..7 of the slice: the B operand of v_mfma_f32_16x16x32."""
+    rng = np.random.default_rng(4)
+    n, k = 16, 128
+    q = rng.integers(-8, 8, size=(n, k))
+    s = O.round_to((rng.random(n) * 0.1 + 1e-3).astype(np.float32), dtype)
+    words = O.plm_layout_int4(O.pack_int4(q)).reshape(64, 4)  # [lane, t]
+    ref = O.round_to(q * s[:, None], dtype)
+    lane = np.arange(64)
+    j = lane % 4
+    sl = s[lane % 16]
+    diag = np.zeros((64, 4))
+    diag[lane, j] = sl
+
+    def f16(bits):  # 16-bit pattern -> value
+        return np.array(bits, np.uint16).view(np.float16).astype(np.float64)
+
+    for t in range(4):
+        w = words[:, t].astype(np.uint64)
+        if dtype == "bf16":
+            half = lambda v, sh: O.bf16_from_bits(((v >> sh) & 0xF) | 0x4300).astype(np.float64)  # noqa: E731
+            a0 = np.stack([half(w, 0), half(w, 16), half(w, 4), half(w, 20)], 1)
+            a1 = np.stack([half(w, 8), half(w, 24), half(w, 12), half(w, 28)], 1)
+            c = np.repeat((-136.0 * sl)[:, None], 4, 1)
+        else:
+            lo = lambda v, sh: f16(((v >> sh) & 0xF) | 0x6400)  # noqa: E731  1024 + u
+            hi = lambda v, sh: f16((((v >> sh) & 0xF) << 4) | 0x5400)  # noqa: E731  64 + u
+            a0 = np.stack([lo(w, 0), lo(w, 16), hi(w, 4), hi(w, 20)], 1)
+            a1 = np.stack([lo(w, 8), lo(w, 24), hi(w, 12), hi(w, 28)], 1)
+            c = np.repeat((np.where(j < 2, -1032.0, -72.0) * sl)[:, None], 4, 1)
+        d = np.concatenate([_mfma4x4x4(a0, diag, c), _mfma4x4x4(a1, diag, c)], 1)  # [lane, 8]
+        got = O.round_to(d.astype(np.float32), dtype)
+        for l in range(64):
+            kk = 32 * t + 8 * (l // 16) + np.arange(8)
+            assert np.array_equal(got[l], ref[l % 16, kk]), (t, l)
 
 
 def test_plm_layout_fp8_known_byte():
