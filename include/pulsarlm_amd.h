@@ -124,6 +124,24 @@ int plm_gemm(plm_format format, const void* x, plm_dtype x_dtype,
              void* y, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * plm_gemm without a workspace argument and without any allocation: for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference. The split-K partial sums and
+ * arrival counters live in a fixed device array of PLM_NOALLOC_SCRATCH_BYTES inside the
+ * library, one per GPU, held until the process ends; the first call on a device takes its
+ * address and clears its counters (a kernel on `stream`). Calls needing more scratch than
+ * that (plm_gemm_workspace_bytes) fail with PLM_ERR_INVALID. Every call on one GPU shares
+ * that GPU's array, so calls that may overlap on one GPU (different streams or threads)
+ * race: use plm_gemm with separate workspaces for those. Same arguments and results as
+ * plm_gemm otherwise.
+ */
+#define PLM_NOALLOC_SCRATCH_BYTES (32 * 1024 * 1024)
+int plm_gemm_noalloc(plm_format format, const void* x, plm_dtype x_dtype,
+                     const void* weight, const void* scale, plm_dtype scale_dtype,
+                     int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                     void* y, void* stream);
+
+/*
  * Per-row dynamic e4m3 quantization of x [M, K] (bf16/fp16, K % 4 == 0):
  * x_scale[m] = max(amax(x[m, :]), 1e-12) / 448, codes[m, k] = e4m3_rne(x[m, k] / x_scale[m]).
  * codes is [M, K] bytes, x_scale fp32 [M]. The rule is the block quantizer of

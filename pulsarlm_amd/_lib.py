@@ -29,6 +29,7 @@ SIGNATURES = {
     "plm_dequant": (_INT, [_INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _P, _INT, _P]),
     "plm_gemm_workspace_bytes": (_I64, [_INT, _I64, _I64, _I64]),
     "plm_gemm": (_INT, [_INT, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ, _P]),
+    "plm_gemm_noalloc": (_INT, [_INT, _P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "plm_quantize_rows_e4m3": (_INT, [_P, _INT, _I64, _I64, _P, _P, _P]),
     "plm_gemm_w8a8_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "plm_gemm_w8a8": (_INT, [_P, _INT, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ, _P]),

@@ -4,6 +4,7 @@
 // where measured faster) and the MFMA kernel.
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 #include "plm_common.hpp"
 
@@ -162,3 +163,82 @@ int plm_gemm_w8a8(const void* x, plm_dtype x_dtype, const void* weight, const vo
 
 }  // extern "C"
 
+
+// ---------------------------------------------------------------------------
+// plm_gemm_noalloc: plm_gemm with its split-K workspace in a fixed device array.
+//
+// `scratch` lives in the code object's static device memory, one copy per GPU the library
+// runs on, held until the process ends. In host code its name is only a stand-in: the
+// device address comes from hipGetSymbolAddress, taken once per device with that device
+// current, and is what the kernels receive. The split-K kernels need the counter region
+// (its first kCounterBytes) zero on entry and leave it zero on exit; set-up clears it once
+// with a fill kernel on the caller's stream (no hipMemsetAsync, so a caller may capture the
+// call). Every call on a GPU shares that GPU's array: calls that overlap on one GPU race.
+// ---------------------------------------------------------------------------
+namespace plm {
+namespace {
+constexpr int64_t kScratchBytes = PLM_NOALLOC_SCRATCH_BYTES;
+static_assert(kScratchBytes >= kCounterBytes && kScratchBytes % 256 == 0, "scratch size");
+__device__ __attribute__((aligned(256))) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices];  // device address of `scratch` per device, once set up
+
+__global__ void __launch_bounds__(256) zero_words_kernel(uint32_t* __restrict__ p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+int scratch_of_current_device(const char* op, hipStream_t s, void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error(op, "no usable current device for the fixed scratch");
+        return PLM_ERR_HIP;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_error(op, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+            return PLM_ERR_HIP;
+        }
+        constexpr int words = static_cast<int>(kCounterBytes / 4);
+        zero_words_kernel<<<(words + 255) / 256, 256, 0, s>>>(static_cast<uint32_t*>(p), words);
+        PLM_HIP_LAUNCH_CHECK(op);
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return PLM_OK;
+}
+}  // namespace
+}  // namespace plm
+
+extern "C" {
+
+int plm_gemm_noalloc(plm_format format, const void* x, plm_dtype x_dtype, const void* weight, const void* scale,
+                     plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
+                     void* y, void* stream) {
+    const char* op = gemm_op_name(format);
+    clear_error();
+    if (int rc = check_gemm(op, format, x, x_dtype, weight, scale, scale_dtype, m, n, k, block_n, group_size, y))
+        return rc;
+    if (m == 0 || n == 0) return PLM_OK;
+    const int64_t need = plm_gemm_workspace_bytes(format, m, n, k);
+    PLM_CHECK_ARG(need <= kScratchBytes, op,
+                  "this call needs %lld bytes of split-K scratch, above the fixed %lld of plm_gemm_noalloc "
+                  "(use plm_gemm with a workspace)",
+                  static_cast<long long>(need), static_cast<long long>(kScratchBytes));
+    hipStream_t s = as_stream(stream);
+    void* ws = nullptr;
+    if (int rc = scratch_of_current_device(op, s, &ws)) return rc;
+    const bool bf16 = x_dtype == PLM_BF16;
+    if (use_decode(m, n))
+        return launch_decode(op, format, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, ws,
+                             static_cast<size_t>(kScratchBytes), s, nullptr, nullptr);
+    return launch_mfma(op, format, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, ws,
+                       static_cast<size_t>(kScratchBytes), s, nullptr, nullptr);
+}
+
+}  // extern "C"
