@@ -31,6 +31,10 @@
 //   scales are found at a fixed stride.
 // * Split-K across workgroups when the output has too few tiles to fill the GPU, reduced
 //   deterministically by the last workgroup to arrive.
+// * Grouped gate_up of the MoE block may fuse the activation: the workgroup's local strips
+//   2p and 2p + 1 are the gate and up strips of one 16-column slice, so every wavefront
+//   holds both halves of its outputs and the epilogue writes act = round(round(silu(g)) *
+//   u) (the unfused silu_mul's expression) instead of the [rows, 2I] gate_up product.
 #include <algorithm>
 #include <type_traits>
 
@@ -59,6 +63,11 @@ struct mfma_args {
     const int32_t* row_index;  // gather: A row r is x[row_index[r]] (null: x[r])
     int64_t w_expert_bytes;
     int64_t s_expert_bytes;
+    // Grouped gate_up with the activation fused (0: off): the weight is [gate; up] with
+    // swiglu_strips 16-column strips each; a workgroup takes gate strip p and up strip
+    // swiglu_strips + p side by side and writes round(round(silu(g)) * u) into y [rows, 16 *
+    // swiglu_strips] instead of the [rows, 2I] product.
+    int swiglu_strips;
 };
 
 namespace {
@@ -124,6 +133,16 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         rows = min(BM, a.m - row0);
     }
     const int strip0 = nb * BS;
+    // SwiGLU (grouped): local strip s is gate strip (s even) or up strip (s odd) of slice
+    // nb * BS / 2 + s / 2; otherwise strip strip0 + s.
+    const bool swiglu = GROUPED && a.swiglu_strips > 0;
+    auto wstrip = [&](int s_local) -> int {
+        if (swiglu) {
+            const int slice = nb * (BS / 2) + (s_local >> 1);
+            return slice < a.swiglu_strips ? slice + ((s_local & 1) ? a.swiglu_strips : 0) : -1;
+        }
+        return strip0 + s_local < a.strips ? strip0 + s_local : -1;
+    };
     const int kt_begin = split * a.tiles_per_split;
     const int kt_end = min(kt_begin + a.tiles_per_split, a.ktiles);
     const uint8_t* wbase = a.w + (GROUPED ? expert * a.w_expert_bytes : 0);
@@ -165,16 +184,24 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         }
         return row_off + c * 16;
     };
-    // Weights: this workgroup's strips are contiguous, ktiles * TB bytes each.
+    // Weights: this workgroup's strips are contiguous, ktiles * TB bytes each (with SwiGLU,
+    // two runs of them, addressed from the expert's first strip).
     const int strip_bytes = a.ktiles * TB;
     const __amdgpu_buffer_rsrc_t b_rsrc =
-        make_rsrc(wbase + static_cast<int64_t>(strip0) * strip_bytes,
-                  static_cast<uint32_t>(min(BS, a.strips - strip0) * strip_bytes));
+        swiglu ? make_rsrc(wbase, static_cast<uint32_t>(a.strips * strip_bytes))
+               : make_rsrc(wbase + static_cast<int64_t>(strip0) * strip_bytes,
+                           static_cast<uint32_t>(min(BS, a.strips - strip0) * strip_bytes));
     int b_off[B_PW > 0 ? B_PW : 1];
 #pragma unroll
     for (int i = 0; i < B_PW; ++i) {
         const int c = wave * B_PW + i;
-        b_off[i] = (c / (TB / 1024)) * strip_bytes + (c % (TB / 1024)) * 1024 + lane * 16;
+        const int sl = c / (TB / 1024), in_strip = (c % (TB / 1024)) * 1024 + lane * 16;
+        if (swiglu) {
+            const int ws = wstrip(sl);
+            b_off[i] = ws >= 0 ? ws * strip_bytes + in_strip : kOOB;
+        } else {
+            b_off[i] = sl * strip_bytes + in_strip;
+        }
     }
 
     auto load_breg = [&](u32x4_t (&dst)[NS][TB / 1024], int kt) {
@@ -202,11 +229,22 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     const bool bf16_scale = a.scale_dtype == PLM_BF16;
     const int s_row = a.groups * a.scale_cols * ES;  // bytes per strip
     const __amdgpu_buffer_rsrc_t s_rsrc =
-        make_rsrc(static_cast<const uint8_t*>(sbase) + static_cast<int64_t>(strip0) * s_row,
-                  static_cast<uint32_t>(min(BS, a.strips - strip0) * s_row));
-    const int s_lane = (a.scale_cols == 1 ? 0 : col16 * ES) + wn * NS * s_row;
+        swiglu ? make_rsrc(sbase, static_cast<uint32_t>(a.strips * s_row))
+               : make_rsrc(static_cast<const uint8_t*>(sbase) + static_cast<int64_t>(strip0) * s_row,
+                           static_cast<uint32_t>(min(BS, a.strips - strip0) * s_row));
+    const int s_lane = a.scale_cols == 1 ? 0 : col16 * ES;
+    int s_strip[NS];  // byte offset of strip j's scales in s_rsrc
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        if (swiglu) {
+            const int ws = wstrip(wn * NS + j);
+            s_strip[j] = ws >= 0 ? ws * s_row : kOOB;
+        } else {
+            s_strip[j] = (wn * NS + j) * s_row;
+        }
+    }
     auto scale_bits = [&](int j, int kt, int t) -> uint32_t {
-        int voff = s_lane + j * s_row, soff = 0;
+        int voff = s_lane + s_strip[j], soff = 0;
         if constexpr (UNIFORM) soff = uniform(kt * kTileK / a.group_size) * a.scale_cols * ES;
         else voff += (kt * kTileK + 32 * t + 8 * kq) / a.group_size * a.scale_cols * ES;
         if constexpr (WIDE) return buffer_load_u32(s_rsrc, voff, soff);
@@ -352,6 +390,26 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         }
     }
 
+    if constexpr (GROUPED && NS % 2 == 0) {
+        if (swiglu) {  // gate strip j, up strip j + 1 of slice nb * BS / 2 + (wn * NS + j) / 2
+            const int inter = a.swiglu_strips * kTileN;
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NS; j += 2) {
+                    const int col = (nb * (BS / 2) + (wn * NS + j) / 2) * kTileN + col16;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int lr = wm * MT * 16 + i * 16 + 4 * kq + r;
+                        if (lr < rows && col < inter)
+                            a.y[static_cast<int64_t>(row0 + lr) * inter + col] = static_cast<uint16_t>(
+                                to_bits16<BF16>(silu_times<BF16>(round_to<BF16>(acc[i][j][r]),
+                                                                 round_to<BF16>(acc[i][j + 1][r]))));
+                    }
+                }
+            return;
+        }
+    }
     // Epilogue: lane holds column col16 of strip (strip0 + wn*NS + j), rows 4*kq + r of m tile i.
 #pragma unroll
     for (int i = 0; i < MT; ++i)
@@ -740,7 +798,7 @@ int grouped_shape_for(int64_t rows, int64_t n_experts) {
 int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                    plm_dtype scale_dtype, int64_t rows, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
                    void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* row_index, int shape,
-                   hipStream_t s) {
+                   hipStream_t s, bool swiglu) {
     PLM_CHECK_ARG(f == PLM_INT4, op, "grouped GEMMs take int4 experts");
     PLM_CHECK_ARG(k <= (int64_t{1} << 21) && rows * k * 2 < kOOB && n * k < (int64_t{1} << 40), op,
                   "problem too large");
@@ -751,6 +809,11 @@ int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const
     a.tiles_per_split = a.ktiles;
     a.m_blocks = 1;
     a.n_blocks = static_cast<int>(ceil_div(a.strips, sh.bs()));
+    if (swiglu) {  // [gate; up] with whole 16-column strips each: slices of bs / 2 strip pairs
+        PLM_CHECK_ARG(n % (2 * kTileN) == 0 && sh.ns % 2 == 0, op, "fused activation needs 16 | intermediate");
+        a.swiglu_strips = static_cast<int>(n / (2 * kTileN));
+        a.n_blocks = static_cast<int>(ceil_div(a.swiglu_strips, sh.bs() / 2));
+    }
     a.tiles = tiles;
     a.row_index = row_index;
     a.w_expert_bytes = ceil_div(n, kTileN) * ceil_div(k, kTileK) * tile_bytes(f);

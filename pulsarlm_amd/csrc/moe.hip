@@ -24,7 +24,7 @@ namespace plm {
 int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                    plm_dtype scale_dtype, int64_t rows, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
                    void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* row_index, int shape,
-                   hipStream_t s);
+                   hipStream_t s, bool swiglu);
 int grouped_block_rows(int shape);
 int grouped_shape_for(int64_t rows, int64_t n_experts);
 
@@ -378,7 +378,7 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(const uint16_t* __restric
         for (int h = 0; h < 2; ++h) {
             const float gv = from_bits16<BF16>((g[q] >> (16 * h)) & 0xffffu);
             const float uv = from_bits16<BF16>((u[q] >> (16 * h)) & 0xffffu);
-            v[h] = round_to<BF16>(gv / (1.f + __expf(-gv))) * uv;
+            v[h] = silu_times<BF16>(gv, uv);
         }
         o[q] = pack2<BF16>(v[0], v[1]);
     }
@@ -520,13 +520,18 @@ int launch_tiles(const char* op, const int32_t* offsets, int64_t n_experts, int6
 
 int launch_plan(const char* op, const grouped_plan& p, const void* x, bool bf16, const void* w, const void* scale,
                 plm_dtype scale_dtype, int64_t rows, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
-                void* y, const int32_t* tiles, const int32_t* row_index, hipStream_t s) {
+                void* y, const int32_t* tiles, const int32_t* row_index, hipStream_t s, bool swiglu = false) {
     if (int rc = launch_grouped(op, PLM_INT4, x, bf16, w, scale, scale_dtype, rows, n, k, block_n, group_size, y,
-                                tiles, p.max_a, row_index, p.shape, s))
+                                tiles, p.max_a, row_index, p.shape, s, swiglu))
         return rc;
     if (!p.two) return PLM_OK;
     return launch_grouped(op, PLM_INT4, x, bf16, w, scale, scale_dtype, rows, n, k, block_n, group_size, y,
-                          tiles + 3 * p.max_a, p.max_b, row_index, p.shape_b, s);
+                          tiles + 3 * p.max_a, p.max_b, row_index, p.shape_b, s, swiglu);
+}
+
+bool fused_swiglu_off() {
+    static const bool off = getenv("PLM_MOE_UNFUSED") != nullptr;  // A/B: separate silu_mul launch
+    return off;
 }
 
 }  // namespace
@@ -623,22 +628,30 @@ int plm_moe(const void* h, plm_dtype dtype, const int32_t* top_experts, const fl
         if (int rc = launch_sort(op, top_experts, top_weights, rows, top_k, n_experts, base, l, offsets, s)) return rc;
         if (int rc = launch_tiles(op, offsets, n_experts, rows, p, tiles, s)) return rc;
     }
-    // gate_up: [rows, 2I] = h[sorted_token] @ gate_up_e^T
-    if (int rc = launch_plan(op, p, h, bf16, gate_up_weight, gate_up_scale, scale_dtype, rows, 2 * intermediate,
-                             hidden, 1, group_size, base + l.gu, tiles,
-                             reinterpret_cast<const int32_t*>(base + l.sorted_token), s))
-        return rc;
-    const int64_t act_n = rows * intermediate;
-    const unsigned act_blocks = static_cast<unsigned>(ceil_div(act_n / 8, 256));
-    if (bf16)
-        silu_mul_kernel<true><<<act_blocks, 256, 0, s>>>(
-            reinterpret_cast<const uint16_t*>(base + l.gu), rows, int(intermediate),
-            reinterpret_cast<uint16_t*>(base + l.act));
-    else
-        silu_mul_kernel<false><<<act_blocks, 256, 0, s>>>(
-            reinterpret_cast<const uint16_t*>(base + l.gu), rows, int(intermediate),
-            reinterpret_cast<uint16_t*>(base + l.act));
-    PLM_HIP_LAUNCH_CHECK(op);
+    if (intermediate % kTileN == 0 && !fused_swiglu_off()) {
+        // gate_up with the activation in its epilogue: act [rows, I] = silu(g) * u directly.
+        if (int rc = launch_plan(op, p, h, bf16, gate_up_weight, gate_up_scale, scale_dtype, rows, 2 * intermediate,
+                                 hidden, 1, group_size, base + l.act, tiles,
+                                 reinterpret_cast<const int32_t*>(base + l.sorted_token), s, true))
+            return rc;
+    } else {
+        // gate_up: [rows, 2I] = h[sorted_token] @ gate_up_e^T, then the activation.
+        if (int rc = launch_plan(op, p, h, bf16, gate_up_weight, gate_up_scale, scale_dtype, rows, 2 * intermediate,
+                                 hidden, 1, group_size, base + l.gu, tiles,
+                                 reinterpret_cast<const int32_t*>(base + l.sorted_token), s))
+            return rc;
+        const int64_t act_n = rows * intermediate;
+        const unsigned act_blocks = static_cast<unsigned>(ceil_div(act_n / 8, 256));
+        if (bf16)
+            silu_mul_kernel<true><<<act_blocks, 256, 0, s>>>(
+                reinterpret_cast<const uint16_t*>(base + l.gu), rows, int(intermediate),
+                reinterpret_cast<uint16_t*>(base + l.act));
+        else
+            silu_mul_kernel<false><<<act_blocks, 256, 0, s>>>(
+                reinterpret_cast<const uint16_t*>(base + l.gu), rows, int(intermediate),
+                reinterpret_cast<uint16_t*>(base + l.act));
+        PLM_HIP_LAUNCH_CHECK(op);
+    }
     // down: [rows, H] = act @ down_e^T
     if (int rc = launch_plan(op, p, base + l.act, bf16, down_weight, down_scale, scale_dtype, rows, hidden,
                              intermediate, 1, group_size, base + l.d, tiles, nullptr, s))

@@ -134,6 +134,14 @@ template <bool BF16> __device__ __forceinline__ uint32_t pack2(float a, float b)
     }
 }
 
+// round(silu(g)) * u for g, u already in the activation dtype: the reference's
+// at::silu(gate) * up (silu = g / (1 + exp(-g)) in fp32, rounded to the dtype before the
+// product; the caller rounds the product). The fused MoE epilogue, the MoE's silu_mul
+// kernel and plm_silu_mul all use this expression, so they give the same bits.
+template <bool BF16> __device__ __forceinline__ float silu_times(float g, float u) {
+    return round_to<BF16>(g / (1.f + expf(-g))) * u;
+}
+
 // Scale load in its stored dtype -> fp32.
 __device__ __forceinline__ float load_scale(const void* base, int64_t index, int dtype) {
     if (dtype == PLM_FP32) return static_cast<const float*>(base)[index];

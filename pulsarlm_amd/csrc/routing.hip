@@ -102,8 +102,8 @@ template <int DT> __device__ __forceinline__ float round_dt(float v) {
 }
 
 template <int DT> __device__ __forceinline__ float silu_mul1(float g, float u) {
-    const float act = round_dt<DT>(g / (1.f + expf(-g)));
-    return round_dt<DT>(act * u);
+    if constexpr (DT == PLM_FP32) return g / (1.f + expf(-g)) * u;
+    else return round_dt<DT>(silu_times<DT == PLM_BF16>(g, u));
 }
 
 template <int DT> __device__ __forceinline__ void store_value(void* p, int64_t i, float v) {

@@ -201,3 +201,34 @@ def test_grouped_gemm_clamps_offsets_to_rows():
     assert_close(y, ref, "offsets past rows")
     y2 = ops.grouped_gemm_int4_cuda(to_dev(x, torch.bfloat16), w, s, to_dev(np.array([5, 3, 3], np.int32)), n, g)
     assert_close(y2[:5], O.gemm_ref(x[:5], deq[0], None), "decreasing offsets")
+
+
+@pytest.mark.parametrize("t,e,hidden,inter,top_k", [(256, 128, 2048, 768, 8), (1024, 8, 256, 128, 2),
+                                                   (40, 8, 256, 128, 2)])
+def test_fused_activation_matches_unfused_pipeline(t, e, hidden, inter, top_k):
+    """routed_experts runs the activation inside the gate_up GEMM's epilogue. Composed
+    from the unfused ops on the same sort -- grouped gate_up GEMM [rows, 2I], silu_mul,
+    grouped down GEMM, then the weighted sum in k order in fp32 -- it must give the same
+    bits (config 5 at T = 256 on one tile shape; 1024 x 2 over 8 experts on the two-level
+    plan of 256-row blocks and 64-row tiles)."""
+    g = 128
+    h, experts, weights, gu, dn = _moe_case(t, e, hidden, inter, top_k, g, seed=t + 11)
+    hd = to_dev(h, torch.bfloat16)
+    out, offsets = ops.routed_experts_int4_cuda(hd, to_dev(experts.astype(np.int32)), to_dev(weights),
+                                                gu[:2], dn[:2], inter, g)
+    order, tokens, _, ref_offsets = O.moe_sort(experts, e)
+    assert np.array_equal(offsets.cpu().numpy(), ref_offsets)
+    rows = hd[torch.from_numpy(tokens).cuda()].contiguous()
+    off = to_dev(ref_offsets)
+    gate_up = ops.grouped_gemm_int4_cuda(rows, gu[0], gu[1], off, 2 * inter, g)
+    act = ops.silu_mul_cuda(gate_up)
+    d = ops.grouped_gemm_int4_cuda(act, dn[0], dn[1], off, hidden, g)
+    position = np.empty(t * top_k, np.int64)
+    position[order] = np.arange(t * top_k)
+    w_bf = torch.from_numpy(weights.reshape(-1)).cuda().to(torch.bfloat16).float()
+    acc = torch.zeros((t, hidden), dtype=torch.float32, device="cuda")
+    pos = torch.from_numpy(position.reshape(t, top_k)).cuda()
+    for j in range(top_k):
+        term = (d[pos[:, j]].float() * w_bf.view(t, top_k)[:, j:j + 1]).to(torch.bfloat16).float()
+        acc = acc + term
+    assert torch.equal(out, acc.to(torch.bfloat16))
