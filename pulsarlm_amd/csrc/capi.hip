@@ -12,7 +12,7 @@ namespace plm {
 int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                   plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
                   void* y, void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq,
-                  const float* x_scale);
+                  const float* x_scale, bool quant_fused = false);
 int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                 plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size, void* y,
                 void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq, const float* x_scale);
@@ -40,6 +40,10 @@ bool use_decode(int64_t m, int64_t n) {
     return m <= 32 && (m <= 24 || ceil_div(n, kTileN) < 4 * cu_count());
 }
 bool use_decode_w8a8(int64_t m) { return m <= 16 && (decode_env_max_m() < 0 || m <= decode_env_max_m()); }
+
+// Environment PLM_W8A8_UNFUSED: always quantize x in its own launch (A/B measurements and
+// the bit-exactness test of the fused quantizer); read on every call.
+bool fused_quant_off() { return getenv("PLM_W8A8_UNFUSED") != nullptr; }
 
 const char* gemm_op_name(plm_format f) { return f == PLM_INT4 ? "gemm_int4_marlin" : "gemm_fp8_marlin"; }
 
@@ -153,6 +157,11 @@ int plm_gemm_w8a8(const void* x, plm_dtype x_dtype, const void* weight, const vo
     auto* sx = reinterpret_cast<float*>(base + l.gemm + l.xq);
     const bool bf16 = x_dtype == PLM_BF16;
     hipStream_t s = as_stream(stream);
+    if (use_decode_w8a8(m) && !fused_quant_off()) {  // M <= 4 with K in LDS: one launch
+        const int rc = launch_decode(op, PLM_FP8, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y,
+                                     base, static_cast<size_t>(l.gemm), s, nullptr, nullptr, true);
+        if (rc != kDecodeNotTaken) return rc;
+    }
     if (int rc = launch_quantize_rows(op, x, bf16, m, k, xq, sx, true, s)) return rc;
     if (use_decode_w8a8(m))
         return launch_decode(op, PLM_FP8, x, bf16, weight, scale, scale_dtype, m, n, k, block_n, group_size, y, base,

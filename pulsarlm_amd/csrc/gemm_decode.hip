@@ -389,6 +389,10 @@ struct rr_args {
     // W8A8: e4m3 x in the quantizer's lane-permuted layout [M][ktiles][128] and row scales.
     const uint8_t* xq;
     const float* x_scale;
+    // W8A8 with the quantizer fused (QF): offset of the wavefront's e4m3 x area in its LDS
+    // area, and of the workgroup's per-wavefront row maxima after all wavefronts' areas.
+    int qx_off, amax_off;
+    int quant_fused;
 };
 
 template <int SC> struct rr_scale {
@@ -401,9 +405,23 @@ template <int SC> struct rr_scale {
 // A8 (W8A8, fp8 weights): x is the per-token e4m3 copy, staged 128 bytes per (row, tile);
 // each tile and strip is one v_mfma_scale_f32_16x16x128_f8f6f4 on the raw weight bytes, its
 // partial scaled by the weight block scale, and the row scales applied at the end.
-template <plm_format F, bool BF16, int SG, int NW, int CH, int SC, bool A8 = false>
-__global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
+//
+// QF (W8A8, M <= 4): the per-token quantizer runs inside this kernel. x is staged in bf16 /
+// fp16 as for W8A16; each wavefront takes the row maxima over its K tiles, the workgroup
+// (which covers all of K) combines them through LDS, and every wavefront rounds its own
+// tiles to e4m3 into the lane-permuted order of the fp8 MFMA operand, with the same
+// arithmetic as plm_quantize_rows_e4m3 (max(amax, 1e-12) / 448, fp32 divide, RNE), so the
+// codes and scales are those of the two-launch path. Every workgroup repeats the row maxima
+// over x (L2 traffic of M * K * 2 bytes per workgroup), which at M <= 4 costs less than
+// the second launch. Its registers are capped at 64 (eight waves per SIMD): uncapped, the
+// quantizer's temporaries took it to 73-75 and one 16-wavefront workgroup per CU, and the
+// second round of workgroups then waits behind the first (measured: 14.3 us instead of
+// 8.2 us at K = 5120, N = 7168). With 3-tile batches (40 tiles over 16 wavefronts) and
+// the end-of-kernel row scales read from LDS, 64 holds without spills.
+template <plm_format F, bool BF16, int SG, int NW, int CH, int SC, bool A8 = false, bool QF = false>
+__global__ void __launch_bounds__(NW * 64, QF ? 8 : 1) decode_rr_kernel(rr_args a) {
     static_assert(!A8 || F == PLM_FP8, "W8A8 takes fp8 weights");
+    static_assert(!QF || (A8 && SG == 1), "the fused quantizer is for W8A8, one strip per workgroup");
     constexpr int TB = fmt_traits<F>::tile_bytes;
     constexpr int NL = TB / 1024;  // 16-byte loads per lane per tile
     constexpr int EB = rr_scale<SC>::eb, CS = rr_scale<SC>::cs, PS = rr_scale<SC>::parts_shift;
@@ -422,7 +440,7 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
     uint8_t* ss = xs + a.x_bytes;
 
     // x: 16-byte chunk j = (row, slot i, column o), LDS [row][slot][256 B] (A8: 128 B of e4m3).
-    if constexpr (A8) {
+    if constexpr (A8 && !QF) {
         const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xq, static_cast<uint32_t>(a.m) * a.ktiles * kTileK);
         const int total = a.m << (a.nkt_shift + 3);
         for (int c = 0; c * 64 < total; ++c) {  // wave-uniform
@@ -473,6 +491,65 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
     for (int sj = 0; sj < SG; ++sj) acc[sj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     const int xrow = min(col16, a.m - 1);
+    // QF: the workgroup's row maxima, [wavefront][4 rows] fp32 after every wavefront's area
+    // (untouched until the kernel ends), and the e4m3 copy of this wavefront's x tiles.
+    [[maybe_unused]] const float* amax_lds = reinterpret_cast<const float*>(rr_lds + a.amax_off);
+    [[maybe_unused]] uint8_t* xq8 = xs + a.qx_off;
+    // Each wavefront's copy of the row scales, [wavefront][4] after the maxima, for the end.
+    [[maybe_unused]] float* scale_lds = reinterpret_cast<float*>(rr_lds + a.amax_off) + NW * 4 + wave * 4;
+    auto row_scale = [&](int r) {
+        float mx = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, amax_lds[w * 4 + r]);
+        return fmaxf(mx, 1e-12f) / 448.f;
+    };
+    auto quantize_x = [&]() {
+        if constexpr (QF) {
+            const int chunks = nkt_w * 16;  // 16-byte chunks per row in this wavefront's tiles
+#pragma unroll 1
+            for (int r = 0; r < (a.m); ++r) {  // wave-uniform
+                float mx = 0.f;
+#pragma unroll 1
+                for (int c = lane; c < chunks; c += 64) {
+                    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(
+                        xs + (((r << a.nkt_shift) + (c >> 4)) << 8) + ((c & 15) << 4));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        mx = fmaxf(mx, fmaxf(fabsf(from_bits16<BF16>(v[j] & 0xffffu)),
+                                             fabsf(from_bits16<BF16>(v[j] >> 16))));
+                }
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+                if (lane == 0) const_cast<float*>(amax_lds)[wave * 4 + r] = mx;
+            }
+            __syncthreads();
+            // Chunk c of a (row, slot) holds K 8c .. 8c + 7 = 32 t + 8 kq + 0..7 with t = c / 4,
+            // kq = c % 4; its codes go to byte 32 kq + 8 t of the slot's 128 bytes.
+            const int per_row = 16 << a.nkt_shift;
+#pragma unroll 1
+            for (int r = 0; r < (a.m); ++r) {  // wave-uniform
+                const float sc = row_scale(r);
+                if (lane == 0) scale_lds[r] = sc;
+#pragma unroll 1
+                for (int j = lane; j < per_row; j += 64) {
+                    const int c = j & 15, slot = (r << a.nkt_shift) + (j >> 4);
+                    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xs + (slot << 8) + (c << 4));
+                    int lo = 0, hi = 0;
+                    lo = __builtin_amdgcn_cvt_pk_fp8_f32(from_bits16<BF16>(v[0] & 0xffffu) / sc,
+                                                         from_bits16<BF16>(v[0] >> 16) / sc, lo, false);
+                    lo = __builtin_amdgcn_cvt_pk_fp8_f32(from_bits16<BF16>(v[1] & 0xffffu) / sc,
+                                                         from_bits16<BF16>(v[1] >> 16) / sc, lo, true);
+                    hi = __builtin_amdgcn_cvt_pk_fp8_f32(from_bits16<BF16>(v[2] & 0xffffu) / sc,
+                                                         from_bits16<BF16>(v[2] >> 16) / sc, hi, false);
+                    hi = __builtin_amdgcn_cvt_pk_fp8_f32(from_bits16<BF16>(v[3] & 0xffffu) / sc,
+                                                         from_bits16<BF16>(v[3] >> 16) / sc, hi, true);
+                    *reinterpret_cast<uint2*>(xq8 + (slot << 7) + 32 * (c & 3) + 8 * (c >> 2)) =
+                        make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+    };
     for (int i0 = 0; i0 < nkt_w; i0 += CH) {  // wave-uniform
         u32x4_t wv[CH][SG][NL];
 #pragma unroll
@@ -489,6 +566,7 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
             // are outstanding, the wavefront's x and scales are in LDS.
             constexpr int kLoads = CH * SG * NL;
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");
+            if constexpr (QF) quantize_x();  // every wavefront gets here (host: ktiles >= NW)
         }
         // int4: every tile's x fragments and (for up to four tiles x strips) scale constants
         // of this batch are read and set up before the first dequant, i.e. while the weight
@@ -532,7 +610,7 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
                 continue;
             }
             if constexpr (A8) {
-                const uint8_t* xp = xs + (((xrow << a.nkt_shift) + i) << 7) + kq * 32;
+                const uint8_t* xp = (QF ? xq8 : xs) + (((xrow << a.nkt_shift) + i) << 7) + kq * 32;
                 const i32x8_t av = __builtin_bit_cast(
                     i32x8_t, u32x8_cat(*reinterpret_cast<const u32x4_t*>(xp), *reinterpret_cast<const u32x4_t*>(xp + 16)));
 #pragma unroll
@@ -578,7 +656,10 @@ __global__ void __launch_bounds__(NW * 64) decode_rr_kernel(rr_args a) {
     if constexpr (A8) {  // row scales (rows 4 kq + r; rows past M are never stored)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float sx = a.x_scale[min(4 * kq + r, a.m - 1)];
+            float sx;
+            // M <= 4: only rows 0..3 are stored.
+            if constexpr (QF) sx = scale_lds[min(r, a.m - 1)];
+            else sx = a.x_scale[min(4 * kq + r, a.m - 1)];
 #pragma unroll
             for (int sj = 0; sj < SG; ++sj) acc[sj][r] *= sx;
         }
@@ -744,6 +825,14 @@ namespace {
 template <plm_format F, bool BF16, int SG, int NW, int CH>
 void launch_rr_t(const rr_args& a, int sc, int grid, size_t lds, hipStream_t s) {
     if constexpr (F == PLM_FP8) {
+        if constexpr (SG == 1) {  // W8A8, quantizer in the kernel (3-tile batches; host: ktiles <= 3 NW)
+            if (a.quant_fused) {
+                if (sc == 0) decode_rr_kernel<F, BF16, SG, NW, 3, 0, true, true><<<grid, NW * 64, lds, s>>>(a);
+                else if (sc == 1) decode_rr_kernel<F, BF16, SG, NW, 3, 1, true, true><<<grid, NW * 64, lds, s>>>(a);
+                else decode_rr_kernel<F, BF16, SG, NW, 3, 2, true, true><<<grid, NW * 64, lds, s>>>(a);
+                return;
+            }
+        }
         if (a.xq != nullptr) {  // W8A8
             if (sc == 0) decode_rr_kernel<F, BF16, SG, NW, CH, 0, true><<<grid, NW * 64, lds, s>>>(a);
             else if (sc == 1) decode_rr_kernel<F, BF16, SG, NW, CH, 1, true><<<grid, NW * 64, lds, s>>>(a);
@@ -823,7 +912,7 @@ bool no_x_staging() {
 int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                   plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
                   void* y, void* workspace, size_t workspace_bytes, hipStream_t s, const uint8_t* xq,
-                  const float* x_scale) {
+                  const float* x_scale, bool quant_fused) {
     const decode_config c = choose_decode(f, m, n, k);
     const layout_dims d = make_dims(n, k, block_n, group_size);
     decode_args a{};
@@ -881,6 +970,7 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
             r.scale_dtype = scale_dtype;
             r.xq = xq;
             r.x_scale = x_scale;
+            r.quant_fused = quant_fused ? 1 : 0;
             while ((int64_t{1} << r.tpg_shift) < tpg) ++r.tpg_shift;
             const int64_t nkt = ceil_div(d.ktiles, rc.nw);
             while ((int64_t{1} << r.nkt_shift) < nkt) ++r.nkt_shift;
@@ -890,12 +980,21 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
             // Scale copies write whole instructions: 64 lanes x (16 or 4) bytes.
             const int64_t cs = eb < 16 ? eb : 16;
             const int64_t s_bytes = round_up(rc.sg * slots * eb, 64 * cs);
-            r.wave_bytes = static_cast<int>(r.x_bytes + s_bytes);
+            // Fused quantizer: the wavefront's e4m3 x after its scales; after every wavefront's
+            // area, the row maxima of all wavefronts, then their row scales (4 rows x fp32).
+            r.qx_off = static_cast<int>(r.x_bytes + s_bytes);
+            const int64_t q_bytes = quant_fused ? round_up(m * slots * kTileK, 1024) : 0;
+            r.wave_bytes = static_cast<int>(r.x_bytes + s_bytes + q_bytes);
+            r.amax_off = rc.nw * r.wave_bytes;
             const int64_t red = int64_t{rc.sg} * rc.nw * 64 * 16;
-            const int64_t lds = std::max<int64_t>(int64_t{rc.nw} * r.wave_bytes, red);
+            const int64_t lds = std::max<int64_t>(int64_t{rc.nw} * r.wave_bytes + (quant_fused ? rc.nw * 32 : 0), red);
             // One batch of loads per wavefront (CH tiles) keeps every load in flight at once.
             const int64_t ch = f == PLM_FP8 ? 4 : (rc.nw == 16 ? 2 : 4);
-            if (lds <= 160 * 1024 && slots <= ch) {
+            // The fused quantizer's barrier needs a tile for every wavefront; its register
+            // budget holds one strip and at most three tiles per wavefront.
+            const bool fused_ok = !quant_fused || (f == PLM_FP8 && m <= 4 && rc.sg == 1 && d.ktiles >= rc.nw &&
+                                                   d.ktiles <= 3 * rc.nw);
+            if (lds <= 160 * 1024 && slots <= ch && fused_ok) {
                 const size_t l = static_cast<size_t>(lds);
                 // CH: tiles per load batch (all of a wavefront's tiles at K = 4096).
                 if (f == PLM_INT4) {
@@ -921,6 +1020,7 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
             }
         }
     }
+    if (quant_fused) return kDecodeNotTaken;
     if (m > 16) {  // two 16-row blocks per MFMA pass (the caller sends W8A8 only up to 16 rows)
         PLM_CHECK_ARG(m <= 32 && xq == nullptr, op, "the decode kernels take at most 32 rows (16 for W8A8)");
         if (f == PLM_INT4) {

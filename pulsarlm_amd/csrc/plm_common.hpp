@@ -278,6 +278,10 @@ template <bool BF16> __device__ __forceinline__ u32x4_t dq_fp8(uint32_t lo, uint
 // access, which is how rows >= M, columns >= K and idle tiles are skipped for free.
 // Offsets at or past kOOB are outside every buffer the kernels build (checked on the host).
 constexpr int kOOB = 0x40000000;
+
+// launch_decode with the fused W8A8 quantizer requested, when its kernel does not apply to
+// the shape (the caller then quantizes in a launch of its own). Not a plm_status value.
+constexpr int kDecodeNotTaken = -1;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
                                              0x00020000);

@@ -9,7 +9,7 @@ import torch
 
 from oracle import oracle as O
 from pulsarlm_amd import ops
-from tests._util import TDT, assert_close, to_dev, to_np
+from tests._util import TDT, assert_close, fp8_case, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -134,3 +134,57 @@ def test_config4_w8a16_m2048_every_row(shape):
     wd = ops.dequant_marlin_cuda("fp8", wt, st, n, k, 128, 128)
     y = ops.gemm_fp8_marlin_cuda(x, wt, st, n, 128, 128)
     print(shape, "rel-L2", _check_full(y, x, wd))
+
+
+_FUSED_SCALES = [(128, np.float32, "bf16"), (16, np.float32, "fp16"), (16, "bf16", "bf16")]
+_FUSED_CASES = ([(m, 5120, 5120, *c) for m in (1, 2, 3, 4) for c in _FUSED_SCALES]
+                + [(m, 4992, 1040, *c) for m in (1, 3) for c in _FUSED_SCALES]
+                + [(m, 2048, 16384, 128, np.float32, "bf16") for m in (1, 4)]
+                + [(3, 5120, 34816, 128, np.float32, "bf16"), (2, 1280, 520, 16, np.float32, "fp16")])
+
+
+@pytest.mark.parametrize("m,k,n,block_n,sdt,dtype", _FUSED_CASES)
+def test_w8a8_fused_quantizer_bit_exact(m, k, n, block_n, sdt, dtype, monkeypatch):
+    """W8A8 at M <= 4 quantizes x inside the GEMM kernel when each wavefront of the
+    workgroup holds one to three K tiles: 16 wavefronts at K = 5120 and 4992 (40 and 39
+    tiles), 8 at N = 16384 (16 tiles). N = 34816 (8 wavefronts, 5 tiles each) and K = 1280
+    (10 tiles for 16) keep the separate quantizer launch. The fused path
+    must give the two-launch result bit for bit (same codes, same row scales, same sums),
+    which PLM_W8A8_UNFUSED selects; both are also checked against the oracle. Row 1 is all
+    zeros (scale 1e-12 / 448) and row 2 spans 2^-12 .. 2^4."""
+    print(f"fused w8a8 m={m} k={k} n={n} block_n={block_n} scale={sdt} x={dtype}", flush=True)
+    rng = np.random.default_rng(m * 7 + k + n)
+    # Every e4m3 code but the NaNs; block scales in [0.01, 0.11), bf16-rounded for bf16.
+    codes, scale = fp8_case(n, k, 128, block_n, seed=m + n)
+    if sdt == "bf16":
+        scale = O.bf16_round(scale)
+        st_in = to_dev(scale, torch.bfloat16)
+    else:
+        st_in = to_dev(scale)
+    wt, st = ops.repack_fp8_marlin_cuda(to_dev(codes).view(torch.float8_e4m3fn), st_in, block_n, 128)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    if m > 1:
+        x[1] = 0.0
+    if m > 2:
+        x[2] *= np.exp2(rng.integers(-12, 5, k))  # 2^16 in scale; small enough for fp16 outputs
+    x = O.round_to(x, dtype)
+    xd = to_dev(x, TDT[dtype])
+    fused = ops.gemm_fp8_w8a8_cuda(xd, wt, st, n, block_n, 128)
+    monkeypatch.setenv("PLM_W8A8_UNFUSED", "1")
+    split = ops.gemm_fp8_w8a8_cuda(xd, wt, st, n, block_n, 128)
+    monkeypatch.delenv("PLM_W8A8_UNFUSED")
+    torch.cuda.synchronize()
+    assert torch.equal(fused, split)
+    # The oracle on the first 1024 output columns (the CPU reference is slow at N = 34816).
+    nc = min(n, 1024)
+    codes, scale, fused = codes[:nc], scale[:-(-nc // block_n)], fused[:, :nc]
+    xc, xs = O.quantize_per_token_e4m3(x)
+    ref = O.gemm_w8a8_ref(xc, xs, codes, scale, block_n, 128, dtype=None)
+    # The fp8 MFMA does not sum its 128 products exactly: it keeps about 2^-15 of the sum
+    # of their magnitudes (measured), which shows where the codes span all of e4m3 and on
+    # row 2. Bound: bf16 output rounding plus 2^-13 of sum |x| |w| over each row.
+    xa = np.abs(O.e4m3_decode(xc).astype(np.float64) * xs[:, None])
+    wa = np.abs(O.dequant_fp8(codes, scale, block_n, 128).astype(np.float64))
+    bound = 2.0**-8 * np.abs(ref) + 2.0**-13 * (xa @ wa.T)
+    err = np.abs(fused.double().cpu().numpy() - ref)
+    assert bool((err <= bound).all()), f"max err / bound {(err / np.maximum(bound, 1e-30)).max():.3g}"

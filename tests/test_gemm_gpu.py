@@ -198,6 +198,7 @@ def test_deterministic_across_calls():
     ("int4", 4096, 4096, 6144),  # MFMA kernel: whole rounds, then the tail as 128-row halves
     ("fp8", 2048, 5120, 34816),  # fp8 W8A16 tall tiles: whole rounds, then the K-split tail launch
     ("w8a8", 16, 5120, 5120),  # per-token quantizer, then the W8A8 decode kernel
+    ("w8a8", 2, 5120, 5120),  # the W8A8 decode kernel with the quantizer fused in
 ])
 def test_gemm_graph_replays_match_eager(case):
     """plm_gemm captured into a graph: the split-K arrival counters are reset by the last
