@@ -140,15 +140,17 @@ _FUSED_SCALES = [(128, np.float32, "bf16"), (16, np.float32, "fp16"), (16, "bf16
 _FUSED_CASES = ([(m, 5120, 5120, *c) for m in (1, 2, 3, 4) for c in _FUSED_SCALES]
                 + [(m, 4992, 1040, *c) for m in (1, 3) for c in _FUSED_SCALES]
                 + [(m, 2048, 16384, 128, np.float32, "bf16") for m in (1, 4)]
-                + [(3, 5120, 34816, 128, np.float32, "bf16"), (2, 1280, 520, 16, np.float32, "fp16")])
+                + [(3, 5120, 34816, 128, np.float32, "bf16"), (2, 1280, 520, 16, np.float32, "fp16"),
+                   (2, 8192, 1040, 128, np.float32, "bf16")])
 
 
 @pytest.mark.parametrize("m,k,n,block_n,sdt,dtype", _FUSED_CASES)
 def test_w8a8_fused_quantizer_bit_exact(m, k, n, block_n, sdt, dtype, monkeypatch):
     """W8A8 at M <= 4 quantizes x inside the GEMM kernel when each wavefront of the
     workgroup holds one to three K tiles: 16 wavefronts at K = 5120 and 4992 (40 and 39
-    tiles), 8 at N = 16384 (16 tiles). N = 34816 (8 wavefronts, 5 tiles each) and K = 1280
-    (10 tiles for 16) keep the separate quantizer launch. The fused path
+    tiles; N = 34816 too, where the unfused kernel takes 8), 8 at N = 16384 (16 tiles).
+    K = 1280 (10 tiles for 16 wavefronts) and K = 8192 (64) keep the separate quantizer
+    launch. The fused path
     must give the two-launch result bit for bit (same codes, same row scales, same sums),
     which PLM_W8A8_UNFUSED selects; both are also checked against the oracle. Row 1 is all
     zeros (scale 1e-12 / 448) and row 2 spans 2^-12 .. 2^4."""
