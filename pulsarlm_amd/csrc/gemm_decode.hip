@@ -404,17 +404,17 @@ template <int SC> struct rr_scale {
 // Maximum of a non-negative float over the wavefront, in lane 63: DPP within each row of 16
 // lanes (swap neighbours, swap pairs, half-row mirror, row mirror), then the row broadcasts
 // carry row 0 into row 1 and rows 0-1 into rows 2-3. No LDS round trips.
+template <int CTRL, int ROW_MASK> __device__ __forceinline__ float dpp_f32(float x) {
+    const int i = __builtin_bit_cast(int, x);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(i, i, CTRL, ROW_MASK, 0xf, false));
+}
 __device__ __forceinline__ float wave_max_to_lane63(float v) {
-    auto dpp = [](float x, int ctrl, int row_mask) {
-        const int i = __builtin_bit_cast(int, x);
-        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(i, i, ctrl, row_mask, 0xf, false));
-    };
-    v = fmaxf(v, dpp(v, 0xB1, 0xf));   // quad_perm [1,0,3,2]
-    v = fmaxf(v, dpp(v, 0x4E, 0xf));   // quad_perm [2,3,0,1]
-    v = fmaxf(v, dpp(v, 0x141, 0xf));  // row_half_mirror
-    v = fmaxf(v, dpp(v, 0x140, 0xf));  // row_mirror
-    v = fmaxf(v, dpp(v, 0x142, 0xa));  // row_bcast:15 into rows 1 and 3
-    v = fmaxf(v, dpp(v, 0x143, 0xc));  // row_bcast:31 into rows 2 and 3
+    v = fmaxf(v, dpp_f32<0xB1, 0xf>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f32<0x4E, 0xf>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f32<0x141, 0xf>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f32<0x140, 0xf>(v));  // row_mirror
+    v = fmaxf(v, dpp_f32<0x142, 0xa>(v));  // row_bcast:15 into rows 1 and 3
+    v = fmaxf(v, dpp_f32<0x143, 0xc>(v));  // row_bcast:31 into rows 2 and 3
     return v;
 }
 

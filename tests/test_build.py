@@ -29,3 +29,15 @@ def test_no_kernel_spills_to_scratch():
                 spilled.append((rep.stem, name, scratch))
     assert total > 0
     assert not spilled, spilled
+
+
+@pytest.mark.skipif(not REPORTS, reason="library not built in this tree")
+def test_reports_are_not_older_than_their_sources():
+    """A failed rebuild leaves the previous report (and library) behind: every report must
+    be at least as new as its source and the shared header."""
+    csrc = BUILD.parent / "csrc"
+    header = (csrc / "plm_common.hpp").stat().st_mtime
+    for rep in REPORTS:
+        src = csrc / (rep.name.replace(".resources.txt", "") + ".hip")
+        if src.exists():
+            assert rep.stat().st_mtime >= max(src.stat().st_mtime, header), f"{rep.name} is older than its sources"

