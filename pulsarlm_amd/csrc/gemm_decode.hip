@@ -404,6 +404,16 @@ template <int SC> struct rr_scale {
 // Maximum of a non-negative float over the wavefront, in lane 63: DPP within each row of 16
 // lanes (swap neighbours, swap pairs, half-row mirror, row mirror), then the row broadcasts
 // carry row 0 into row 1 and rows 0-1 into rows 2-3. No LDS round trips.
+// x / s rounded to fp32 as the IEEE divide would for the quantizer's operands, from the
+// reciprocal inv = 1 / s: q = x * inv, then one correction with the exact residual
+// fma(-q, s, x), and x's sign (so -0 stays -0). An exhaustive check over every bf16 and
+// fp16 x with |x| <= amax and every 16-bit amax (s = max(amax, 1e-12) / 448) finds the e4m3
+// codes identical to those of x / s (the fp32 values differ only below 2^-60).
+__device__ __forceinline__ float div_by_scale(float x, float s, float inv) {
+    const float q = x * inv;
+    return copysignf(__builtin_fmaf(__builtin_fmaf(-q, s, x), inv, q), x);
+}
+
 template <int CTRL, int ROW_MASK> __device__ __forceinline__ float dpp_f32(float x) {
     const int i = __builtin_bit_cast(int, x);
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(i, i, CTRL, ROW_MASK, 0xf, false));
@@ -545,20 +555,18 @@ __global__ void __launch_bounds__(NW * 64, QF ? 8 : 1) decode_rr_kernel(rr_args 
 #pragma unroll 1
             for (int r = 0; r < (a.m); ++r) {  // wave-uniform
                 const float sc = row_scale(r);
+                const float inv = 1.f / sc;
                 if (lane == 0) scale_lds[r] = sc;
 #pragma unroll 1
                 for (int j = lane; j < per_row; j += 64) {
                     const int c = j & 15, slot = (r << a.nkt_shift) + (j >> 4);
                     const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xs + (slot << 8) + (c << 4));
+                    auto div = [&](uint32_t bits) { return div_by_scale(from_bits16<BF16>(bits), sc, inv); };
                     int lo = 0, hi = 0;
-                    lo = __builtin_amdgcn_cvt_pk_fp8_f32(from_bits16<BF16>(v[0] & 0xffffu) / sc,
-                                                         from_bits16<BF16>(v[0] >> 16) / sc, lo, false);
-                    lo = __builtin_amdgcn_cvt_pk_fp8_f32(from_bits16<BF16>(v[1] & 0xffffu) / sc,
-                                                         from_bits16<BF16>(v[1] >> 16) / sc, lo, true);
-                    hi = __builtin_amdgcn_cvt_pk_fp8_f32(from_bits16<BF16>(v[2] & 0xffffu) / sc,
-                                                         from_bits16<BF16>(v[2] >> 16) / sc, hi, false);
-                    hi = __builtin_amdgcn_cvt_pk_fp8_f32(from_bits16<BF16>(v[3] & 0xffffu) / sc,
-                                                         from_bits16<BF16>(v[3] >> 16) / sc, hi, true);
+                    lo = __builtin_amdgcn_cvt_pk_fp8_f32(div(v[0] & 0xffffu), div(v[0] >> 16), lo, false);
+                    lo = __builtin_amdgcn_cvt_pk_fp8_f32(div(v[1] & 0xffffu), div(v[1] >> 16), lo, true);
+                    hi = __builtin_amdgcn_cvt_pk_fp8_f32(div(v[2] & 0xffffu), div(v[2] >> 16), hi, false);
+                    hi = __builtin_amdgcn_cvt_pk_fp8_f32(div(v[3] & 0xffffu), div(v[3] >> 16), hi, true);
                     *reinterpret_cast<uint2*>(xq8 + (slot << 7) + 32 * (c & 3) + 8 * (c >> 2)) =
                         make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
                 }
