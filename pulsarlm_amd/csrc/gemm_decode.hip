@@ -52,7 +52,34 @@ struct decode_args {
     const float* x_scale;
     // x staged in LDS (M <= 4): bytes per row and per wavefront of the staging area.
     int xs_row, xs_wave;
+    // W8A8 with the quantizer fused (QF): nonzero selects it; the row maxima and row scales
+    // of the workgroup follow the wavefronts' staging areas in LDS.
+    int quant_fused;
 };
+
+// x / s rounded to fp32 as the IEEE divide would for the quantizer's operands, from the
+// reciprocal inv = 1 / s: q = x * inv, then one correction with the exact residual
+// fma(-q, s, x), and x's sign (so -0 stays -0). An exhaustive check over every bf16 and
+// fp16 x with |x| <= amax and every 16-bit amax (s = max(amax, 1e-12) / 448) finds the e4m3
+// codes identical to those of x / s (the fp32 values differ only below 2^-60).
+__device__ __forceinline__ float div_by_scale(float x, float s, float inv) {
+    const float q = x * inv;
+    return copysignf(__builtin_fmaf(__builtin_fmaf(-q, s, x), inv, q), x);
+}
+
+template <int CTRL, int ROW_MASK> __device__ __forceinline__ float dpp_f32(float x) {
+    const int i = __builtin_bit_cast(int, x);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(i, i, CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_max_to_lane63(float v) {
+    v = fmaxf(v, dpp_f32<0xB1, 0xf>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f32<0x4E, 0xf>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f32<0x141, 0xf>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f32<0x140, 0xf>(v));  // row_mirror
+    v = fmaxf(v, dpp_f32<0x142, 0xa>(v));  // row_bcast:15 into rows 1 and 3
+    v = fmaxf(v, dpp_f32<0x143, 0xc>(v));  // row_bcast:31 into rows 2 and 3
+    return v;
+}
 
 // One wavefront's batch of TPW K tiles for SP strips: weights, raw scale bits and x (RB
 // blocks of 16 rows).
@@ -79,10 +106,18 @@ template <plm_format F, int SP, int TPW, bool A8, int RB> struct decode_batch {
 // RB = 2 (16 < M <= 32, bf16/fp16 x read from global memory): each dequantized weight
 // fragment feeds two MFMAs, one per 16-row block, so the weights are still read and
 // dequantized once.
+//
+// QF (W8A8, M <= 4, one workgroup over all of K, every wavefront with a tile): the
+// per-token quantizer runs inside the kernel, as in decode_rr_kernel. x is staged in
+// bf16 / fp16 (XS); each wavefront takes the row maxima over its K range, the workgroup
+// combines them through LDS, and each wavefront rewrites its staged x in place as e4m3 in
+// the fp8 MFMA operand's lane order (128 bytes per row and tile), from which the A
+// fragments are read. Same codes and row scales as plm_quantize_rows_e4m3.
 template <plm_format F, bool BF16, int SP, int TPW, int NW, bool UNIFORM, bool WIDE, bool A8 = false, bool XS = false,
-          int RB = 1>
+          int RB = 1, bool QF = false>
 __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
     static_assert(RB == 1 || (!A8 && !XS), "two row blocks: bf16/fp16 x read from global memory only");
+    static_assert(!QF || (A8 && XS && UNIFORM && RB == 1), "the fused quantizer stages bf16/fp16 x in LDS");
     constexpr int TB = fmt_traits<F>::tile_bytes;
     constexpr int ES = WIDE ? 4 : 2;  // scale element bytes
     const int lane = threadIdx.x & 63;
@@ -109,14 +144,14 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
                           static_cast<uint32_t>(a.groups * a.scale_cols * ES));
     }
     const __amdgpu_buffer_rsrc_t xr =
-        A8 ? make_rsrc(a.xq, static_cast<uint32_t>(a.m) * a.ktiles * kTileK)
+        (A8 && !QF) ? make_rsrc(a.xq, static_cast<uint32_t>(a.m) * a.ktiles * kTileK)
            : make_rsrc(a.x, static_cast<uint32_t>(a.m) * a.k * 2);
     // bf16/fp16: row * K * 2 + 16 kq (+ 64 t + 256 kt); e4m3: row * ktiles * 128 + 32 kq (+ 128 kt).
     int x_lane[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         const int row = 16 * rb + col16;
-        x_lane[rb] = A8 ? (row < a.m ? row * a.ktiles * kTileK : kOOB) + 32 * kq
+        x_lane[rb] = (A8 && !QF) ? (row < a.m ? row * a.ktiles * kTileK : kOOB) + 32 * kq
                         : (row < a.m ? row * a.k * 2 : kOOB) + 16 * kq;
     }
     const int w_lane = lane * 16;
@@ -154,7 +189,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
                     else b.s[tt][j] = buffer_load_u16(sr[j], s_lane, s_off);
                 }
             }
-            if constexpr (A8) {
+            if constexpr (A8 && !QF) {
                 b.x[tt][0][0] = buffer_load16(xr, x_lane[0], x_off);
                 b.x[tt][0][1] = buffer_load16(xr, x_lane[0] + 16, x_off);
             } else if constexpr (!XS) {
@@ -211,10 +246,19 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
             const int kt = kt0 + tt;
             if (kt >= w_hi) break;  // wave-uniform
             if constexpr (A8) {  // x past K is already zero in the quantized copy
+                u32x4_t x0, x1;
+                if constexpr (QF) {  // e4m3 rows of xs_row / 2 bytes in the wavefront's area
+                    const uint8_t* xp = xs_wave + min(col16, a.m - 1) * (a.xs_row >> 1) + (kt - w_lo) * kTileK + kq * 32;
+                    x0 = *reinterpret_cast<const u32x4_t*>(xp);
+                    x1 = *reinterpret_cast<const u32x4_t*>(xp + 16);
+                } else {
+                    x0 = b.x[tt][0][0];
+                    x1 = b.x[tt][0][1];
+                }
 #pragma unroll
                 for (int j = 0; j < SP; ++j) {
                     const float s = scale_from_bits<WIDE>(b.s[tt][j], bf16_scale);
-                    const i32x8_t av = __builtin_bit_cast(i32x8_t, u32x8_cat(b.x[tt][0][0], b.x[tt][0][1]));
+                    const i32x8_t av = __builtin_bit_cast(i32x8_t, u32x8_cat(x0, x1));
                     const i32x8_t bv = __builtin_bit_cast(i32x8_t, u32x8_cat(b.w[tt][j][0], b.w[tt][j][TB / 1024 - 1]));
                     const f32x4_t part = mfma16x16x128_fp8(av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
@@ -279,6 +323,57 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
 
     // One batch in flight per wavefront; latency is hidden by the other resident
     // wavefronts (a register double buffer gets rotated into copies that wait).
+    // QF: the workgroup's row maxima [NW][4] and each wavefront's copy of the row scales
+    // [NW][4] after the staging areas.
+    [[maybe_unused]] float* amax_lds = reinterpret_cast<float*>(xs_lds + NW * a.xs_wave);
+    [[maybe_unused]] float* scale_lds = amax_lds + NW * 4 + wave * 4;
+    auto quantize_x = [&]() {
+        if constexpr (QF) {
+            const int chunks = a.xs_row >> 4;  // 16-byte chunks per staged row (16 per tile)
+#pragma unroll 1
+            for (int r = 0; r < a.m; ++r) {  // wave-uniform
+                float mx = 0.f;
+#pragma unroll 1
+                for (int c = lane; c < chunks; c += 64) {
+                    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xs_wave + r * a.xs_row + c * 16);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        mx = fmaxf(mx, fmaxf(fabsf(from_bits16<BF16>(v[j] & 0xffffu)),
+                                             fabsf(from_bits16<BF16>(v[j] >> 16))));
+                }
+                mx = wave_max_to_lane63(mx);
+                if (lane == 63) amax_lds[wave * 4 + r] = mx;
+            }
+            __syncthreads();
+            // In place: chunk j (row j / chunks, K 8 (j % chunks) .. + 7) is read from byte
+            // 16 j and its 8 codes go to byte 128 (j / 16) + 32 (j % 4) + 8 ((j / 4) % 4),
+            // never past a byte this or an earlier pass has read.
+#pragma unroll 1
+            for (int r = 0; r < a.m; ++r) {  // wave-uniform
+                float mx = 0.f;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) mx = fmaxf(mx, amax_lds[w * 4 + r]);
+                const float sc = fmaxf(mx, 1e-12f) / 448.f;
+                const float inv = 1.f / sc;
+                if (lane == 0) scale_lds[r] = sc;
+#pragma unroll 1
+                for (int c = lane; c < chunks; c += 64) {
+                    const int j = r * chunks + c;
+                    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xs_wave + j * 16);
+                    auto div = [&](uint32_t bits) { return div_by_scale(from_bits16<BF16>(bits), sc, inv); };
+                    int lo = 0, hi = 0;
+                    lo = __builtin_amdgcn_cvt_pk_fp8_f32(div(v[0] & 0xffffu), div(v[0] >> 16), lo, false);
+                    lo = __builtin_amdgcn_cvt_pk_fp8_f32(div(v[1] & 0xffffu), div(v[1] >> 16), lo, true);
+                    hi = __builtin_amdgcn_cvt_pk_fp8_f32(div(v[2] & 0xffffu), div(v[2] >> 16), hi, false);
+                    hi = __builtin_amdgcn_cvt_pk_fp8_f32(div(v[3] & 0xffffu), div(v[3] >> 16), hi, true);
+                    *reinterpret_cast<uint2*>(xs_wave + 128 * (j >> 4) + 32 * (j & 3) + 8 * ((j >> 2) & 3)) =
+                        make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+    };
+
     decode_batch<F, SP, TPW, A8, RB> b;
     for (int kt = w_lo; kt < w_hi; kt += TPW) {
         load_batch(b, kt);
@@ -288,13 +383,16 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(decode_args a) {
             // landed. Later batches find it long done.
             constexpr int kBatchLoads = TPW * SP * (fmt_traits<F>::tile_bytes / 1024 + (UNIFORM ? 1 : 0));
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kBatchLoads) : "memory");
+            if constexpr (QF) {
+                if (kt == w_lo) quantize_x();  // every wavefront has a tile (checked on the host)
+            }
         }
         compute_batch(b, kt);
     }
     if constexpr (A8) {  // row scales; rows past M are never stored
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float sx = a.x_scale[min(4 * kq + i, a.m - 1)];
+            const float sx = QF ? scale_lds[min(4 * kq + i, a.m - 1)] : a.x_scale[min(4 * kq + i, a.m - 1)];
 #pragma unroll
             for (int j = 0; j < SP; ++j) acc[0][j][i] *= sx;
         }
@@ -404,29 +502,6 @@ template <int SC> struct rr_scale {
 // Maximum of a non-negative float over the wavefront, in lane 63: DPP within each row of 16
 // lanes (swap neighbours, swap pairs, half-row mirror, row mirror), then the row broadcasts
 // carry row 0 into row 1 and rows 0-1 into rows 2-3. No LDS round trips.
-// x / s rounded to fp32 as the IEEE divide would for the quantizer's operands, from the
-// reciprocal inv = 1 / s: q = x * inv, then one correction with the exact residual
-// fma(-q, s, x), and x's sign (so -0 stays -0). An exhaustive check over every bf16 and
-// fp16 x with |x| <= amax and every 16-bit amax (s = max(amax, 1e-12) / 448) finds the e4m3
-// codes identical to those of x / s (the fp32 values differ only below 2^-60).
-__device__ __forceinline__ float div_by_scale(float x, float s, float inv) {
-    const float q = x * inv;
-    return copysignf(__builtin_fmaf(__builtin_fmaf(-q, s, x), inv, q), x);
-}
-
-template <int CTRL, int ROW_MASK> __device__ __forceinline__ float dpp_f32(float x) {
-    const int i = __builtin_bit_cast(int, x);
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(i, i, CTRL, ROW_MASK, 0xf, false));
-}
-__device__ __forceinline__ float wave_max_to_lane63(float v) {
-    v = fmaxf(v, dpp_f32<0xB1, 0xf>(v));   // quad_perm [1,0,3,2]
-    v = fmaxf(v, dpp_f32<0x4E, 0xf>(v));   // quad_perm [2,3,0,1]
-    v = fmaxf(v, dpp_f32<0x141, 0xf>(v));  // row_half_mirror
-    v = fmaxf(v, dpp_f32<0x140, 0xf>(v));  // row_mirror
-    v = fmaxf(v, dpp_f32<0x142, 0xa>(v));  // row_bcast:15 into rows 1 and 3
-    v = fmaxf(v, dpp_f32<0x143, 0xc>(v));  // row_bcast:31 into rows 2 and 3
-    return v;
-}
 
 //
 // A8 (W8A8, fp8 weights): x is the per-token e4m3 copy, staged 128 bytes per (row, tile);
@@ -787,6 +862,14 @@ void launch_decode_t(const decode_args& a, int strip_groups, bool uniform, hipSt
         }
         return;
     }
+    if constexpr (F == PLM_FP8 && SP == 1 && TPW == 2 && NW == 16) {
+        if (a.quant_fused) {  // W8A8 with the quantizer in the kernel (conditions: launch_decode)
+            const size_t lds = static_cast<size_t>(NW) * a.xs_wave + NW * 32;
+            if (wide) decode_kernel<F, BF16, SP, TPW, NW, true, true, true, true, 1, true><<<grid, NW * 64, lds, s>>>(a);
+            else decode_kernel<F, BF16, SP, TPW, NW, true, false, true, true, 1, true><<<grid, NW * 64, lds, s>>>(a);
+            return;
+        }
+    }
     if constexpr (F == PLM_FP8) {
         if (a.xq != nullptr) {  // W8A8 (group_size % 128 == 0 is checked by the caller)
             if (wide) decode_kernel<F, BF16, SP, TPW, NW, true, true, true><<<grid, NW * 64, 0, s>>>(a);
@@ -1048,7 +1131,21 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
             }
         }
     }
-    if (quant_fused) return kDecodeNotTaken;
+    if (quant_fused) {
+        // The split-K kernel with the quantizer fused: one workgroup over all of K (the row
+        // maxima stay inside it), x staged in LDS, every wavefront with a tile (all reach the
+        // barrier), and the one instantiation (one strip, two-tile batches, 16 wavefronts).
+        const int per_wave = static_cast<int>(ceil_div(c.tiles_per_split, c.nw));
+        const bool ok = f == PLM_FP8 && m <= kStageMaxM && a.xs_wave > 0 && c.splits == 1 && uniform && c.sp == 1 &&
+                        c.tpw == 2 && c.nw == 16 && (c.nw - 1) * per_wave < c.tiles_per_split &&
+                        static_cast<int64_t>(c.nw) * a.xs_wave + c.nw * 32 <= 64 * 1024 * 2;
+        if (!ok) return kDecodeNotTaken;
+        a.quant_fused = 1;
+        if (bf16) launch_decode_f<PLM_FP8, true>(a, c, uniform, s);
+        else launch_decode_f<PLM_FP8, false>(a, c, uniform, s);
+        PLM_HIP_LAUNCH_CHECK(op);
+        return PLM_OK;
+    }
     if (m > 16) {  // two 16-row blocks per MFMA pass (the caller sends W8A8 only up to 16 rows)
         PLM_CHECK_ARG(m <= 32 && xq == nullptr, op, "the decode kernels take at most 32 rows (16 for W8A8)");
         if (f == PLM_INT4) {

@@ -141,7 +141,9 @@ _FUSED_CASES = ([(m, 5120, 5120, *c) for m in (1, 2, 3, 4) for c in _FUSED_SCALE
                 + [(m, 4992, 1040, *c) for m in (1, 3) for c in _FUSED_SCALES]
                 + [(m, 2048, 16384, 128, np.float32, "bf16") for m in (1, 4)]
                 + [(3, 5120, 34816, 128, np.float32, "bf16"), (2, 1280, 520, 16, np.float32, "fp16"),
-                   (2, 8192, 1040, 128, np.float32, "bf16")])
+                   (2, 8192, 1040, 128, np.float32, "bf16")]
+                + [(1, 17408, 5120, *c) for c in _FUSED_SCALES]
+                + [(2, 17408, 4096, 128, np.float32, "fp16"), (3, 17408, 5120, 128, np.float32, "bf16")])
 
 
 @pytest.mark.parametrize("m,k,n,block_n,sdt,dtype", _FUSED_CASES)
@@ -150,7 +152,8 @@ def test_w8a8_fused_quantizer_bit_exact(m, k, n, block_n, sdt, dtype, monkeypatc
     workgroup holds one to three K tiles: 16 wavefronts at K = 5120 and 4992 (40 and 39
     tiles; N = 34816 too, where the unfused kernel takes 8), 8 at N = 16384 (16 tiles).
     K = 1280 (10 tiles for 16 wavefronts) and K = 8192 (64) keep the separate quantizer
-    launch. The fused path
+    launch. K = 17408 runs the split-K decode kernel: fused at M <= 2 (one workgroup over
+    all of K, x staged in LDS), separate at M = 3 (x too large to stage). The fused path
     must give the two-launch result bit for bit (same codes, same row scales, same sums),
     which PLM_W8A8_UNFUSED selects, wherever both run the same wavefront count; both are
     also checked against the oracle. Row 1 is all
