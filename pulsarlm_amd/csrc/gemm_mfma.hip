@@ -60,6 +60,7 @@ struct mfma_args {
     const float* x_scale;   // [M]
     // Grouped
     const int32_t* tiles;      // [max_tiles][3]: expert, first row, rows (rows == 0: idle)
+    const int32_t* tile_count;  // the number of real tiles (a prefix of `tiles`)
     const int32_t* row_index;  // gather: A row r is x[row_index[r]] (null: x[r])
     int64_t w_expert_bytes;
     int64_t s_expert_bytes;
@@ -119,8 +120,18 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     // Work tile: (row block, column block), grouped: (expert tile, column block).
     int nb, expert = 0, row0, rows;
     if constexpr (GROUPED) {
-        const int tile = blockIdx.x / a.n_blocks;
-        nb = blockIdx.x % a.n_blocks;
+        // Workgroups are dealt to the 8 XCDs round-robin by id. The real (tile, column
+        // block) items are given out in 8 contiguous runs, one per XCD, so the column
+        // blocks of a row tile (the same x rows) and the consecutive tiles of an expert
+        // (the same weights) run on one XCD and share its L2; ids past the real items exit.
+        const int items = uniform(*a.tile_count) * a.n_blocks;
+        const int per_xcd = (items + 7) >> 3;
+        const int idx = blockIdx.x >> 3;
+        if (idx >= per_xcd) return;
+        const int item = (blockIdx.x & 7) * per_xcd + idx;
+        if (item >= items) return;
+        const int tile = item / a.n_blocks;
+        nb = item % a.n_blocks;
         expert = a.tiles[3 * tile];
         row0 = a.tiles[3 * tile + 1];
         rows = a.tiles[3 * tile + 2];
@@ -797,8 +808,8 @@ int grouped_shape_for(int64_t rows, int64_t n_experts) {
 
 int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                    plm_dtype scale_dtype, int64_t rows, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
-                   void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* row_index, int shape,
-                   hipStream_t s, bool swiglu) {
+                   void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* tile_count,
+                   const int32_t* row_index, int shape, hipStream_t s, bool swiglu) {
     PLM_CHECK_ARG(f == PLM_INT4, op, "grouped GEMMs take int4 experts");
     PLM_CHECK_ARG(k <= (int64_t{1} << 21) && rows * k * 2 < kOOB && n * k < (int64_t{1} << 40), op,
                   "problem too large");
@@ -815,10 +826,11 @@ int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const
         a.n_blocks = static_cast<int>(ceil_div(a.swiglu_strips, sh.bs() / 2));
     }
     a.tiles = tiles;
+    a.tile_count = tile_count;
     a.row_index = row_index;
     a.w_expert_bytes = ceil_div(n, kTileN) * ceil_div(k, kTileK) * tile_bytes(f);
     a.s_expert_bytes = static_cast<int64_t>(a.strips) * a.groups * a.scale_cols * dtype_size(scale_dtype);
-    dim3 grid(static_cast<unsigned>(max_tiles * a.n_blocks), 1);
+    dim3 grid(static_cast<unsigned>(round_up(max_tiles * a.n_blocks, 8)), 1);  // whole XCD rounds
     const bool uniform = group_size % kTileK == 0;
     const bool wide = scale_dtype == PLM_FP32;
     const int mode = (bf16 ? 4 : 0) + (uniform ? 2 : 0) + (wide ? 1 : 0);

@@ -23,7 +23,8 @@ namespace plm {
 
 int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                    plm_dtype scale_dtype, int64_t rows, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
-                   void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* row_index, int shape,
+                   void* y, const int32_t* tiles, int64_t max_tiles, const int32_t* tile_count, const int32_t* row_index,
+                   int shape,
                    hipStream_t s, bool swiglu);
 int grouped_block_rows(int shape);
 int grouped_shape_for(int64_t rows, int64_t n_experts);
@@ -144,7 +145,7 @@ __device__ __forceinline__ void expert_rows(const int32_t* __restrict__ offsets,
 // written at the expert's tile prefix; slots past the last tile get rows = 0.
 __global__ void __launch_bounds__(1024) moe_tiles_kernel(const int32_t* __restrict__ offsets, int n_experts,
                                                           int32_t rows, int bm, int64_t max_tiles,
-                                                          int32_t* __restrict__ tiles) {
+                                                          int32_t* __restrict__ tiles, int32_t* __restrict__ count) {
     __shared__ int32_t buf[1024];
     __shared__ int32_t first_tile[4096];
     for (int e = threadIdx.x; e < n_experts; e += 1024) {
@@ -154,6 +155,7 @@ __global__ void __launch_bounds__(1024) moe_tiles_kernel(const int32_t* __restri
     }
     __syncthreads();
     const int32_t n_tiles = block_exclusive_scan(first_tile, n_experts, buf);
+    if (threadIdx.x == 0) *count = static_cast<int32_t>(min<int64_t>(n_tiles, max_tiles));
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
         int32_t lo, hi;
         expert_rows(offsets, e, rows, lo, hi);
@@ -184,7 +186,8 @@ constexpr int kSmallSortChunks = 128;   // chunks (8 per wavefront), so rows <= 
 __global__ void __launch_bounds__(1024) moe_sort_small_kernel(
     const int32_t* __restrict__ experts, const float* __restrict__ weights, int rows, int top_k, int n_experts,
     int n_chunks, int bm, int64_t max_tiles, int32_t* __restrict__ sorted_token, float* __restrict__ sorted_weight,
-    int32_t* __restrict__ position, int32_t* __restrict__ offsets, int32_t* __restrict__ tiles) {
+    int32_t* __restrict__ position, int32_t* __restrict__ offsets, int32_t* __restrict__ tiles,
+    int32_t* __restrict__ count) {
     __shared__ int32_t tab[kSmallSortTable];
     __shared__ int32_t buf[1024];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -292,6 +295,7 @@ __global__ void __launch_bounds__(1024) moe_sort_small_kernel(
     }
     __syncthreads();
     const int32_t n_tiles = block_exclusive_scan(tab, n_experts, buf);
+    if (tid == 0) *count = static_cast<int32_t>(min<int64_t>(n_tiles, max_tiles));
 #pragma unroll
     for (int q = 0; q < kExpertsPerThread; ++q) {
         const int e = tid + 1024 * q;
@@ -323,7 +327,7 @@ __device__ __forceinline__ void tiles2_split(int32_t c, int bb, int full, int32_
 __global__ void __launch_bounds__(1024) moe_tiles2_kernel(const int32_t* __restrict__ offsets, int n_experts,
                                                            int32_t rows, int bb, int sb, int full, int64_t max_big,
                                                            int64_t max_small, int32_t* __restrict__ big,
-                                                           int32_t* __restrict__ small) {
+                                                           int32_t* __restrict__ small, int32_t* __restrict__ counts) {
     __shared__ int32_t buf[1024];
     __shared__ int32_t first_big[4096];
     __shared__ int32_t first_small[4096];
@@ -337,6 +341,10 @@ __global__ void __launch_bounds__(1024) moe_tiles2_kernel(const int32_t* __restr
     __syncthreads();
     const int32_t n_big = block_exclusive_scan(first_big, n_experts, buf);
     const int32_t n_small = block_exclusive_scan(first_small, n_experts, buf);
+    if (threadIdx.x == 0) {
+        counts[0] = static_cast<int32_t>(min<int64_t>(n_big, max_big));
+        counts[1] = static_cast<int32_t>(min<int64_t>(n_small, max_small));
+    }
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
         int32_t nbig, rem, lo, hi;
         expert_rows(offsets, e, rows, lo, hi);
@@ -434,7 +442,7 @@ moe_ws moe_layout(int64_t tokens, int64_t top_k, int64_t n_experts, int64_t hidd
     w.sorted_token = take(rows * 4);
     w.sorted_weight = take(rows * 4);
     w.position = take(rows * 4);
-    w.tiles = take(max_tiles * 12);
+    w.tiles = take(max_tiles * 12 + 8);  // the tile lists, then their tile counts
     w.gu = take(rows * 2 * inter * 2);
     w.act = take(rows * inter * 2);
     w.d = take(rows * hidden * 2);
@@ -454,6 +462,8 @@ struct grouped_plan {
     int bb, sb, full;     // two lists: big and small block rows, rows that count as a full big block
     int64_t max_a, max_b;  // tile slots of the first and second list
     int64_t slots() const { return max_a + max_b; }
+    // The tile lists' real tile counts (list a, list b) follow the lists: int32 index.
+    int64_t count_at() const { return 3 * slots(); }
 };
 
 grouped_plan plan_grouped(int64_t rows, int64_t n_experts) {
@@ -510,10 +520,10 @@ int launch_tiles(const char* op, const int32_t* offsets, int64_t n_experts, int6
                  int32_t* tiles, hipStream_t s) {
     if (p.two)
         moe_tiles2_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), int32_t(rows), p.bb, p.sb, p.full, p.max_a, p.max_b, tiles,
-                                             tiles + 3 * p.max_a);
+                                             tiles + 3 * p.max_a, tiles + p.count_at());
     else
         moe_tiles_kernel<<<1, 1024, 0, s>>>(offsets, int(n_experts), int32_t(rows), grouped_block_rows(p.shape),
-                                            p.max_a, tiles);
+                                            p.max_a, tiles, tiles + p.count_at());
     PLM_HIP_LAUNCH_CHECK(op);
     return PLM_OK;
 }
@@ -522,11 +532,11 @@ int launch_plan(const char* op, const grouped_plan& p, const void* x, bool bf16,
                 plm_dtype scale_dtype, int64_t rows, int64_t n, int64_t k, int64_t block_n, int64_t group_size,
                 void* y, const int32_t* tiles, const int32_t* row_index, hipStream_t s, bool swiglu = false) {
     if (int rc = launch_grouped(op, PLM_INT4, x, bf16, w, scale, scale_dtype, rows, n, k, block_n, group_size, y,
-                                tiles, p.max_a, row_index, p.shape, s, swiglu))
+                                tiles, p.max_a, tiles + p.count_at(), row_index, p.shape, s, swiglu))
         return rc;
     if (!p.two) return PLM_OK;
     return launch_grouped(op, PLM_INT4, x, bf16, w, scale, scale_dtype, rows, n, k, block_n, group_size, y,
-                          tiles + 3 * p.max_a, p.max_b, row_index, p.shape_b, s, swiglu);
+                          tiles + 3 * p.max_a, p.max_b, tiles + p.count_at() + 1, row_index, p.shape_b, s, swiglu);
 }
 
 bool fused_swiglu_off() {
@@ -560,7 +570,7 @@ int plm_grouped_gemm(plm_format format, const void* x, plm_dtype x_dtype, const 
     PLM_CHECK_ARG(aligned(x, 16) && aligned(weight, 16), op, "x and weight must be 16-byte aligned");
     PLM_CHECK_ARG(format == PLM_INT4, op, "grouped GEMMs take int4 experts");
     const grouped_plan p = plan_grouped(rows, n_experts);
-    const int64_t need = kCounterBytes + p.slots() * 12;
+    const int64_t need = kCounterBytes + p.slots() * 12 + 8;
     if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need) {
         set_error(op, "workspace of %lld bytes required, %zu given", static_cast<long long>(need), workspace_bytes);
         return PLM_ERR_WORKSPACE;
@@ -574,7 +584,7 @@ int plm_grouped_gemm(plm_format format, const void* x, plm_dtype x_dtype, const 
 
 int64_t plm_grouped_gemm_workspace_bytes(int64_t rows, int64_t n_experts) {
     if (rows <= 0 || n_experts <= 0) return kCounterBytes;
-    return kCounterBytes + plan_grouped(rows, n_experts).slots() * 12;
+    return kCounterBytes + plan_grouped(rows, n_experts).slots() * 12 + 8;
 }
 
 int64_t plm_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t n_experts, int64_t hidden,
@@ -622,7 +632,7 @@ int plm_moe(const void* h, plm_dtype dtype, const int32_t* top_experts, const fl
             top_experts, top_weights, int(rows), int(top_k), int(n_experts), int(chunks64),
             grouped_block_rows(p.shape), p.max_a, reinterpret_cast<int32_t*>(base + l.sorted_token),
             reinterpret_cast<float*>(base + l.sorted_weight), reinterpret_cast<int32_t*>(base + l.position), offsets,
-            tiles);
+            tiles, tiles + p.count_at());
         PLM_HIP_LAUNCH_CHECK(op);
     } else {
         if (int rc = launch_sort(op, top_experts, top_weights, rows, top_k, n_experts, base, l, offsets, s)) return rc;
