@@ -159,7 +159,9 @@ int64_t plm_gemm_w8a8_workspace_bytes(int64_t m, int64_t n, int64_t k);
  * and multiplied with e4m3 weights on the fp8 MFMA:
  * y[m, n] = x_scale[m] * sum_g s[n, g] * sum_{k in g} e4m3(xq[m, k]) * e4m3(w[n, k]).
  * group_size must be a multiple of 128. No counterpart in the reference (its fp8
- * path is W8A16, gemm_fp8_marlin_cuda); x and y bf16 or fp16.
+ * path is W8A16, gemm_fp8_marlin_cuda); x and y bf16 or fp16. At M <= 4 (M <= 2 for
+ * long K) the quantization runs inside the GEMM kernel (one launch, the same codes,
+ * scales and result); otherwise it is a launch of its own into the workspace.
  */
 int plm_gemm_w8a8(const void* x, plm_dtype x_dtype,
                   const void* weight, const void* scale, plm_dtype scale_dtype,
