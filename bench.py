@@ -273,6 +273,23 @@ def section_prefill(b: Bench):
                                    "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 3)}
         del copies
     out["aggregate_TFLOP/s"] = round(tot_flop / tot_t / 1e12, 1)
+    out["vendor_bf16_reference"] = vendor_bf16_reference(b)
+    return out
+
+
+def vendor_bf16_reference(b: Bench):
+    """A reference point, not this library: torch.matmul (the ROCm BLAS) on dense bf16
+    weights of the same shapes at M=4096 -- no quantization, no dequant, 4x the weight
+    bytes. Fractions of the same bf16 dense peak."""
+    torch = b.torch
+    out = {}
+    for name, k, n in SHAPES:
+        x = torch.randn(4096, k, device=b.dev).to(torch.bfloat16)
+        w = torch.randn(n, k, device=b.dev).to(torch.bfloat16)
+        y = torch.empty(4096, n, device=b.dev, dtype=torch.bfloat16)
+        tt = b.time([lambda: torch.matmul(x, w.t(), out=y)], reps=4)
+        out[f"{name}_m4096"] = {"us": round(tt * 1e6, 1), "frac_mfma": round(2 * 4096 * n * k / tt / 1e12 / BF16_PEAK_TFLOPS, 3)}
+        del x, w, y
     return out
 
 
