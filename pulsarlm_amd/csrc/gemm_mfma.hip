@@ -102,6 +102,8 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     static_assert(A_STAGE % 1024 == 0 && B_STAGE % 1024 == 0, "stages are whole 1 KiB chunks");
     constexpr int ST = UNIFORM ? 1 : 4;  // scale values per strip per K step
     constexpr int ES = WIDE ? 4 : 2;     // scale element bytes
+    // Software-pipelined x fragments (see the K loop), for the one-row tall shapes.
+    constexpr bool PIPE_A = F == PLM_INT4 && UNIFORM && !A8 && WM == 1 && MT >= 8;
 
     // Two stages of [A tile | weight tiles]. Stage s holds K step kt_begin + s (mod 2); the
     // loads of step kt + 1 go straight from HBM into the other stage while step kt computes.
@@ -319,6 +321,38 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
                     const f32x4_t part = mfma16x16x128_fp8(av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(scale_from_bits<WIDE>(sc[j][0], bf16_scale), part[r], acc[i][j][r]);
+                }
+            }
+        } else if constexpr (PIPE_A) {
+            // The MT x fragments of a K slice are held in registers and each is re-read for
+            // the next slice right after its MFMAs, so a fragment read has a whole slice of
+            // MFMAs (MT * NS) to land instead of the next two.
+            auto frag = [&](int i, int t) {
+                const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
+                return *reinterpret_cast<const u32x4_t*>(ra + (((4 * t + kq) ^ col16) * 16));
+            };
+            u32x4_t af[MT];
+#pragma unroll
+            for (int i = 0; i < MT; ++i) af[i] = frag(i, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                u32x4_t b[NS];
+#pragma unroll
+                for (int j = 0; j < NS; ++j) {
+                    const float raw = scale_from_bits<WIDE>(sc[j][UNIFORM ? 0 : t], bf16_scale);
+                    if constexpr (F == PLM_INT4) {
+                        b[j] = dq_int4<BF16>(wv[j][0][t], make_int4_scale<BF16>(raw));
+                    } else {
+                        b[j] = dq_fp8<BF16>(wv[j][t >> 1][(t & 1) * 2], wv[j][t >> 1][(t & 1) * 2 + 1],
+                                            round_to<BF16>(raw));
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < MT; ++i) {
+#pragma unroll
+                    for (int j = 0; j < NS; ++j) acc[i][j] = mfma16x16x32<BF16>(af[i], b[j], acc[i][j]);
+                    if (t < 3) af[i] = frag(i, t + 1);
+                    __builtin_amdgcn_sched_barrier(0);  // keep the read here, a slice ahead
                 }
             }
         } else {
