@@ -103,7 +103,10 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     constexpr int ST = UNIFORM ? 1 : 4;  // scale values per strip per K step
     constexpr int ES = WIDE ? 4 : 2;     // scale element bytes
     // Software-pipelined x fragments (see the K loop), for the one-row tall shapes.
-    constexpr bool PIPE_A = F == PLM_INT4 && UNIFORM && !A8 && WM == 1 && MT >= 8;
+    constexpr bool PIPE_A = UNIFORM && !A8 && WM == 1 && MT >= 8;
+    // Fragments kept a slice ahead: all MT, or 12 for fp8, whose weight tiles already hold
+    // two K steps of registers (16 would spill).
+    constexpr int PD = F == PLM_FP8 ? MT - 4 : MT;
 
     // Two stages of [A tile | weight tiles]. Stage s holds K step kt_begin + s (mod 2); the
     // loads of step kt + 1 go straight from HBM into the other stage while step kt computes.
@@ -331,9 +334,9 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
                 const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
                 return *reinterpret_cast<const u32x4_t*>(ra + (((4 * t + kq) ^ col16) * 16));
             };
-            u32x4_t af[MT];
+            u32x4_t af[PD];
 #pragma unroll
-            for (int i = 0; i < MT; ++i) af[i] = frag(i, 0);
+            for (int i = 0; i < PD; ++i) af[i] = frag(i, 0);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 u32x4_t b[NS];
@@ -348,11 +351,17 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
                     }
                 }
 #pragma unroll
-                for (int i = 0; i < MT; ++i) {
+                for (int i = 0; i < PD; ++i) {
 #pragma unroll
                     for (int j = 0; j < NS; ++j) acc[i][j] = mfma16x16x32<BF16>(af[i], b[j], acc[i][j]);
                     if (t < 3) af[i] = frag(i, t + 1);
                     __builtin_amdgcn_sched_barrier(0);  // keep the read here, a slice ahead
+                }
+#pragma unroll
+                for (int i = PD; i < MT; ++i) {
+                    const u32x4_t a1 = frag(i, t);
+#pragma unroll
+                    for (int j = 0; j < NS; ++j) acc[i][j] = mfma16x16x32<BF16>(a1, b[j], acc[i][j]);
                 }
             }
         } else {
