@@ -78,7 +78,9 @@ template <bool A8> struct a_traits {
     static constexpr int slots = row_bytes / 16;                 // its 16-byte slots
 };
 
-template <plm_format F, bool BF16, bool UNIFORM, bool WIDE, bool A8, bool GROUPED, int WM, int WN, int MT, int NS>
+// VO: the 16-byte epilogue (see its comment) is compiled in; the host selects it per launch.
+template <plm_format F, bool BF16, bool UNIFORM, bool WIDE, bool A8, bool GROUPED, int WM, int WN, int MT, int NS,
+          bool VO = false>
 __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     constexpr int NW = WM * WN;  // wavefronts
     constexpr int NT = NW * 64;
@@ -465,6 +467,43 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         }
     }
     // Epilogue: lane holds column col16 of strip (strip0 + wn*NS + j), rows 4*kq + r of m tile i.
+    // With 16-byte aligned output rows, each m tile goes through the wavefront's own LDS area
+    // (16 rows of 16 * NS columns; the row pitch is padded by 16 bytes so the four row groups
+    // of one write land in different banks) and leaves as one 16-byte store per 8 columns of a
+    // row, instead of a 2-byte store per element. Separate instantiations (VO) for the launches
+    // that take it: compiled into the split-K kernels too, it changed their register
+    // allocation and made down at M = 1024 10 % slower.
+    if (VO && a.splits == 1 && (a.n & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
+        constexpr int EROW = 32 * NS + 16;
+        static_assert(1024 + NW * 16 * EROW <= 2 * STAGE, "epilogue staging fits the stages");
+        __syncthreads();  // every wavefront is past the K loop's last reads of the stages
+        uint8_t* ew = lds + 1024 + wave * 16 * EROW;  // past the split-K arrival flag
+        const int col0 = (strip0 + wn * NS) * kTileN;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+            for (int j = 0; j < NS; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    *reinterpret_cast<uint16_t*>(ew + (4 * kq + r) * EROW + (16 * j + col16) * 2) =
+                        static_cast<uint16_t>(to_bits16<BF16>(acc[i][j][r]));
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int c0 = 0; c0 < 32 * NS; c0 += 64) {  // 16 rows x 2 * NS chunks of 8 columns
+                const int c = c0 + lane;
+                if (c < 32 * NS) {
+                    const int row = c / (2 * NS), ch = c % (2 * NS);
+                    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ew + row * EROW + ch * 16);
+                    const int lr = wm * MT * 16 + i * 16 + row;
+                    const int col = col0 + ch * 8;
+                    if (lr < rows && col < a.n)
+                        *reinterpret_cast<u32x4_t*>(a.y + static_cast<int64_t>(row0 + lr) * a.n + col) = v;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -632,6 +671,8 @@ int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k, bool
 namespace {
 template <plm_format F, bool BF16, bool UNIFORM, bool WIDE, bool A8, bool GROUPED>
 void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
+    // The 16-byte epilogue for the unsplit tall shapes.
+    [[maybe_unused]] const bool vo = a.splits == 1 && (a.n & 7) == 0 && aligned(a.y, 16);
     if constexpr (!A8 && !GROUPED) {
         if (shape == 9) {
             mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kLarge8.wm, kLarge8.wn, kLarge8.mt, kLarge8.ns>
@@ -663,8 +704,12 @@ void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
             return;
         }
         if (shape == 10) {
-            mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kTallHalf.wm, kTallHalf.wn, kTallHalf.mt, kTallHalf.ns>
-                <<<grid, kTallHalf.wm * kTallHalf.wn * 64, 0, s>>>(a);
+            if (vo)
+                mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kTallHalf.wm, kTallHalf.wn, kTallHalf.mt, kTallHalf.ns,
+                            true><<<grid, kTallHalf.wm * kTallHalf.wn * 64, 0, s>>>(a);
+            else
+                mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kTallHalf.wm, kTallHalf.wn, kTallHalf.mt, kTallHalf.ns>
+                    <<<grid, kTallHalf.wm * kTallHalf.wn * 64, 0, s>>>(a);
             return;
         }
         if (shape == 8) {
@@ -673,8 +718,12 @@ void launch_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
             return;
         }
         if (shape == 6) {
-            mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kTall.wm, kTall.wn, kTall.mt, kTall.ns>
-                <<<grid, kTall.wm * kTall.wn * 64, 0, s>>>(a);
+            if (vo)
+                mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kTall.wm, kTall.wn, kTall.mt, kTall.ns, true>
+                    <<<grid, kTall.wm * kTall.wn * 64, 0, s>>>(a);
+            else
+                mfma_kernel<F, BF16, UNIFORM, WIDE, A8, GROUPED, kTall.wm, kTall.wn, kTall.mt, kTall.ns>
+                    <<<grid, kTall.wm * kTall.wn * 64, 0, s>>>(a);
             return;
         }
     }
@@ -803,7 +852,7 @@ void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t 
 #define PLM_GROUPED_CASE(i)                                                                                   \
     case i:                                                                                                   \
         mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kGroupedShapes[i].wm, kGroupedShapes[i].wn,         \
-                    kGroupedShapes[i].mt, kGroupedShapes[i].ns>                                               \
+                    kGroupedShapes[i].mt, kGroupedShapes[i].ns, true>                                         \
             <<<grid, kGroupedShapes[i].wm * kGroupedShapes[i].wn * 64, 0, s>>>(a);                            \
         break;
     switch (shape) {
@@ -814,7 +863,7 @@ void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t 
         PLM_GROUPED_CASE(5)
         PLM_GROUPED_CASE(6)
         default:
-            mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kHuge.wm, kHuge.wn, kHuge.mt, kHuge.ns>
+            mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kHuge.wm, kHuge.wn, kHuge.mt, kHuge.ns, true>
                 <<<grid, kHuge.wm * kHuge.wn * 64, 0, s>>>(a);
     }
 #undef PLM_GROUPED_CASE
