@@ -328,6 +328,29 @@ def test_full_size_against_gpu_fp32(shape, m):
     print(shape, m, "rel-L2", _check_full(y, x, wd))
 
 
+@pytest.mark.parametrize("n", [1024, 1000, 1004])
+@pytest.mark.parametrize("y_shift", [0, 1])
+def test_mfma_epilogue_store_forms(n, y_shift, monkeypatch):
+    """The tall shape stores its output 16 bytes at a time when N % 8 == 0 and y is 16-byte
+    aligned, and element by element otherwise (y need only be 2-byte aligned; N = 1004 and a
+    y one element past an aligned address take the fallback). Both forms must give the
+    aligned call's result on the same shape bit for bit, and every row must match the fp32
+    reference."""
+    m, k = 512, 512  # 8 tall tiles, K not split (the split-K kernels keep the 2-byte stores)
+    monkeypatch.setenv("PLM_MFMA", "X")
+    x, packed, s = _full_case(m, k, n, seed=n + y_shift)
+    w, sc = ops.repack_int4_marlin_cuda(packed, s, 1, 128)
+    wd = ops.dequant_marlin_cuda("int4", w, sc, n, k, 1, 128)
+    buf = torch.full((m * n + 16,), float("nan"), dtype=torch.bfloat16, device=x.device)
+    y = buf[y_shift:y_shift + m * n].view(m, n)
+    ops.gemm_int4_marlin_cuda(x, w, sc, n, 1, 128, out=y)
+    torch.cuda.synchronize()
+    _check_full(y, x, wd)
+    assert bool(buf[:y_shift].isnan().all()) and bool(buf[y_shift + m * n:].isnan().all()), "wrote outside y"
+    ref = ops.gemm_int4_marlin_cuda(x, w, sc, n, 1, 128)  # a fresh, aligned y
+    assert torch.equal(y, ref)
+
+
 def test_decode_and_mfma_kernels_agree():
     """M=16 and M=32 run the decode kernels (one and two 16-row blocks), M=33 the MFMA
     kernel; their common rows must agree to the GEMM tolerance (each is checked against the
