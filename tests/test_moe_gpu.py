@@ -68,6 +68,28 @@ def test_grouped_gemm_matches_per_expert_reference(counts):
     assert_close(y, ref, f"grouped {counts}")
 
 
+@pytest.mark.parametrize("counts", [[5, 0, 17, 1, 0, 40, 3, 34], [700, 130, 0, 200, 0, 0, 300, 0]])
+@pytest.mark.parametrize("n", [520, 516])
+def test_grouped_gemm_unaligned_output(counts, n):
+    """The grouped kernels store 16 bytes at a time when N % 8 == 0 and y is 16-byte aligned,
+    element by element otherwise: a y one element past an aligned address (and N = 516) must
+    give the aligned result bit for bit and leave the rest of its buffer untouched. The
+    second count list takes the two-list plan (256-row blocks, then 64-row tiles)."""
+    e, k, g = 8, 1024, 128
+    w, s, _ = _experts(e, n, k, g, seed=n + sum(counts))
+    rows = sum(counts)
+    x = to_dev(O.bf16_round(np.random.default_rng(rows).standard_normal((rows, k)).astype(np.float32)),
+               torch.bfloat16)
+    offsets = to_dev(np.cumsum(counts).astype(np.int32))
+    ref = ops.grouped_gemm_int4_cuda(x, w, s, offsets, n, g)
+    buf = torch.full((rows * n + 16,), float("nan"), dtype=torch.bfloat16, device=x.device)
+    y = buf[1:1 + rows * n].view(rows, n)
+    ops.grouped_gemm_int4_cuda(x, w, s, offsets, n, g, out=y)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+    assert bool(buf[:1].isnan().all()) and bool(buf[1 + rows * n:].isnan().all()), "wrote outside y"
+
+
 # The 16-row grouped tiles (at most 8 rows per expert on average) and the 32-row ones (9-24)
 # across scale storage, activation dtype and 256-wide groups, with an expert spanning several
 # tiles and a ragged N.
