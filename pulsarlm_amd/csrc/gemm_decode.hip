@@ -809,8 +809,17 @@ decode_config choose_decode(plm_format f, int64_t m, int64_t n, int64_t k) {
     // and two K tiles per batch; 16 wavefronts split K.
     const int64_t groups4 = ceil_div(strips, 4);
     const int64_t wgs4 = groups4 * std::min<int64_t>(ceil_div(cus, groups4), std::max<int64_t>(1, ktiles / 16));
+    // fp8 (2 KiB tiles) at M > 4, measured at the Qwen3-27B-like shapes: four-strip groups
+    // when their workgroups, with the K split they get, fit one round of the CUs (o: 240) or K
+    // is long enough that two-strip wavefronts would chain many load batches (down, 136 K
+    // tiles); otherwise two strips on 8 wavefronts (qkv: 336 four-strip workgroups would take
+    // two rounds; 15.4 -> 12.9 us at M=16, and o 12.6 -> 10.0 us the other way).
+    const int64_t wgs4_split = groups4 * std::min<int64_t>(ceil_div(cus, groups4), ceil_div(ktiles, 16));
     if (strips >= 4 * cus) {
         c.sp = 2, c.tpw = 1, c.nw = 16;
+    } else if (f == PLM_FP8 && m > 4 && ktiles >= 32) {
+        if (wgs4_split <= cus || ktiles >= 96) c.sp = 4, c.tpw = 1, c.nw = 16;
+        else c.sp = 2, c.tpw = 1, c.nw = 8;
     } else if (m > 4 && ktiles >= 32 && 4 * wgs4 >= 3 * cus) {
         c.sp = 4, c.tpw = 1, c.nw = 16;
     } else if (m > 4) {
@@ -830,7 +839,6 @@ decode_config choose_decode(plm_format f, int64_t m, int64_t n, int64_t k) {
     }
     if (c.sp == 4 && (c.tpw != 1 || c.nw != 16)) c.sp = 2;  // four strips: one instantiation only
     if (c.sp > 1) c.tpw = 1;                                 // two tiles per batch: one strip only
-    (void)f;
     c.strip_groups = static_cast<int>(ceil_div(strips, c.sp));
     // Split K across workgroups only when the column blocks alone cannot fill the GPU.
     int64_t splits = 1;
