@@ -985,7 +985,13 @@ struct rr_config {
 // strip per workgroup, 16 wavefronts, or 8 when the strips alone give every CU four
 // workgroups. M > 4 (x fills most of LDS, one workgroup per CU): strips grouped so that
 // there is about one workgroup per CU.
-rr_config choose_rr(int64_t m, int64_t n, int64_t k) {
+// fp8 (2 KiB tiles) differs from int4 at the Qwen3-27B-like shapes (a sweep of every setting
+// at M=1 and M=16): W8A16 at M <= 4 with fewer than 4 strips per CU takes two strips per
+// workgroup when those fit one round of the CUs (o 8.3 -> 7.9 us, qkv 9.0 -> 8.6 us), and
+// W8A8 above M=4 with many strips one strip on 8 wavefronts (gate_up at M=16 42.8 -> 39.0
+// us). W8A8 at M <= 4 keeps one strip per workgroup for its fused quantizer (a two-strip
+// fused variant measured slower: qkv 9.0 -> 9.7 us).
+rr_config choose_rr(int64_t m, int64_t n, int64_t k, plm_format f, bool a8) {
     rr_config c;
     if (m > 16) return c;
     const int64_t strips = ceil_div(n, kTileN);
@@ -994,6 +1000,9 @@ rr_config choose_rr(int64_t m, int64_t n, int64_t k) {
     c.nw = 16;
     if (m <= 4) {
         if (strips >= 4 * cus) c.nw = 8;
+        else if (f == PLM_FP8 && !a8 && ceil_div(strips, 2) <= cus) c.sg = 2;
+    } else if (f == PLM_FP8 && a8 && strips >= 4 * cus) {
+        c.nw = 8;
     } else {
         c.sg = 6;
         for (int sg : {1, 2, 3, 4}) {
@@ -1069,7 +1078,7 @@ int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const 
     const int64_t tpg = group_size / kTileK;
     const int sc_mode = d.scale_cols == 16 ? (scale_dtype == PLM_FP32 ? 1 : 0) : (scale_dtype == PLM_FP32 ? 2 : -1);
     if (uniform && (tpg & (tpg - 1)) == 0 && sc_mode >= 0 && !no_x_staging()) {
-        rr_config rc = choose_rr(m, n, k);
+        rr_config rc = choose_rr(m, n, k, f, xq != nullptr || quant_fused);
         // The fused quantizer takes at most three tiles per wavefront: 16 wavefronts where 8
         // would hold more (measured at N = 34816, K = 5120: 34.2 us, against 35.2 us for the
         // separate quantizer launch and 8 wavefronts).
