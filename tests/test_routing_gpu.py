@@ -69,6 +69,34 @@ def test_silu_mul_matches_oracle(dtype, tokens, n):
         assert np.mean(to_np(y) == ref) > 0.99
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_silu_every_16bit_value(dtype):
+    """The 16-bit silu (the reference's g / (1 + expf(-g)) in fp32, moe_routing.cu:129, then
+    rounded) over every bf16 value with |g| <= 100 and every finite fp16 value, against the
+    oracle: at most one unit in the last place apart, at least 99.9 % exact (zeros compared by
+    value), and exact for g from -88.7 to -87.3, where silu's fp32 value is just above the
+    denormal range and bf16 keeps it (a reciprocal-based silu flushes it to zero there)."""
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    if dtype == "bf16":
+        g = (bits << 16).view(np.float32)
+        g = g[np.isfinite(g) & (np.abs(g) <= 100)]
+    else:
+        g = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+        g = g[np.isfinite(g)]
+    n = g.size
+    x = np.stack([g, np.ones_like(g)]).reshape(1, 2 * n)  # one row [g | u = 1]
+    y = to_np(ops.silu_mul_cuda(to_dev(x, TDTYPE[dtype]))).reshape(-1)
+    ref = O.silu_mul_ref(x, dtype).reshape(-1)
+    assert np.mean(y == ref) >= 0.999, np.mean(y == ref)
+    tdt = TDTYPE[dtype]
+    as_int = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(tdt).view(torch.int16).numpy().astype(np.int32)
+    # Zeros compare by value (-0 == +0; adding +0 makes every zero +0): one ulp apart at most.
+    assert int(np.abs(as_int(y + np.float32(0)) - as_int(ref + np.float32(0))).max()) <= 1
+    band = (g >= -88.7) & (g <= -87.3)
+    if dtype == "bf16":
+        assert band.any() and np.array_equal(y[band], ref[band]), (y[band], ref[band])
+
+
 def test_router_feeds_the_moe_block():
     """route_top_k (int32 experts) -> routed_experts with int4 experts, on one stream,
     against the oracle's routing and routed_experts_ref."""
