@@ -197,6 +197,7 @@ def test_deterministic_across_calls():
     ("int4", 256, 4096, 4096),  # MFMA kernel with a K split (fewer tiles than CUs)
     ("int4", 4096, 4096, 6144),  # MFMA kernel: whole rounds, then the tail as 128-row halves
     ("fp8", 2048, 5120, 34816),  # fp8 W8A16 tall tiles: whole rounds, then the K-split tail launch
+    ("fp8", 16, 5120, 7168),  # fp8 W8A16 decode: two strips on 8 wavefronts, K split in two
     ("w8a8", 16, 5120, 5120),  # per-token quantizer, then the W8A8 decode kernel
     ("w8a8", 2, 5120, 5120),  # the W8A8 decode kernel with the quantizer fused in
 ])
