@@ -125,11 +125,12 @@ def _moe_case(t, e, hidden, inter, top_k, g, seed):
 
 @pytest.mark.parametrize("t,e,hidden,inter,top_k", [(40, 8, 256, 128, 2), (1, 8, 256, 128, 2), (256, 128, 2048, 768, 8),
                                                    (16, 1024, 128, 128, 8), (1024, 128, 256, 128, 8),
-                                                   (70, 3, 128, 128, 3)])
+                                                   (70, 3, 128, 128, 3), (33, 1, 128, 128, 1), (300, 1, 128, 128, 1)])
 def test_routed_experts_matches_oracle(t, e, hidden, inter, top_k):
     """Up to 8192 rows with one tile shape, the sort runs as one workgroup (a ballot-plane rank per
     64-row chunk and a scan of the experts x chunks table); 1024 x 128 fills that table,
-    and 16 x 1024 spreads few rows over many experts."""
+    and 16 x 1024 spreads few rows over many experts. One expert: every row in one run (300
+    rows take the two-list plan: a full 256-row block, then 64-row tiles)."""
     g = 128
     h, experts, weights, gu, dn = _moe_case(t, e, hidden, inter, top_k, g, seed=t + e)
     out, offsets = ops.routed_experts_int4_cuda(to_dev(h, torch.bfloat16), to_dev(experts.astype(np.int32)),
