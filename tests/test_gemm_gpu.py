@@ -132,6 +132,20 @@ def test_int4_gemm_group_sizes(m, g):
     assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, g), None), f"m={m} g={g}")
 
 
+@pytest.mark.parametrize("m", [1, 17, 40, 300])
+@pytest.mark.parametrize("n,k", [(8, 16), (40, 32), (24, 48), (200, 16)])
+def test_int4_gemm_below_one_k_tile(m, n, k):
+    """K below one 128-wide tile (16-wide groups, the reference test's group size) and N below
+    or not a multiple of a 16-column strip, on the decode kernels (M <= 32) and the MFMA
+    kernel (M > 32): the partial K tile and the partial strip read as zero."""
+    g = 16
+    packed, s = int4_case(n, k, g, 1, seed=n + k)
+    w, sc = _repack_int4(packed, s, 1, g)
+    x = x_case(m, k, "bf16", seed=m + k)
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, torch.bfloat16), w, sc, n, 1, g)
+    assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, g), None), f"m={m} n={n} k={k}")
+
+
 @pytest.mark.parametrize("m", [1, 3, 4, 8, 13, 16])
 @pytest.mark.parametrize("case", ["fp16s-bf16x", "fp32s-bf16x", "bf16s-fp16x", "fp32s-strip", "g256"])
 def test_decode_kernel_variants(m, case):
