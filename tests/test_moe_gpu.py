@@ -255,3 +255,29 @@ def test_fused_activation_matches_unfused_pipeline(t, e, hidden, inter, top_k):
         term = (d[pos[:, j]].float() * w_bf.view(t, top_k)[:, j:j + 1]).to(torch.bfloat16).float()
         acc = acc + term
     assert torch.equal(out, acc.to(torch.bfloat16))
+
+
+def test_empty_inputs_every_entry_point():
+    """Zero rows through every entry point besides the int4 GEMM (covered with the GEMM
+    tests): each returns an empty result of the right shape without launching anything
+    that could read past its inputs."""
+    from tests.test_fp8_gpu import _fp8_weights
+    k, n, e, g, inter = 256, 128, 4, 128, 128
+    _, _, wt, st = _fp8_weights(n, k, seed=3)
+    x0 = torch.empty((0, k), dtype=torch.bfloat16, device="cuda")
+    assert ops.gemm_fp8_marlin_cuda(x0, wt, st, n, 128, 128).shape == (0, n)
+    assert ops.gemm_fp8_w8a8_cuda(x0, wt, st, n, 128, 128).shape == (0, n)
+    codes, scale = ops.quantize_rows_e4m3_cuda(x0)
+    assert codes.shape == (0, k) and scale.shape == (0,)
+    w, s, _ = _experts(e, n, k, g, seed=4)
+    offsets = torch.zeros(e, dtype=torch.int32, device="cuda")
+    assert ops.grouped_gemm_int4_cuda(x0, w, s, offsets, n, g).shape == (0, n)
+    gu_w, gu_s, _ = _experts(e, 2 * inter, k, g, seed=5)
+    dn_w, dn_s, _ = _experts(e, k, inter, g, seed=6)
+    out, _ = ops.routed_experts_int4_cuda(x0, torch.empty((0, 2), dtype=torch.int32, device="cuda"),
+                                          torch.empty((0, 2), dtype=torch.float32, device="cuda"),
+                                          (gu_w, gu_s), (dn_w, dn_s), inter, g)
+    assert out.shape == (0, k)
+    weights, chosen = ops.route_top_k_cuda(torch.empty((0, e), device="cuda"), 2)
+    assert weights.shape == (0, 2) and chosen.shape == (0, 2)
+    assert ops.silu_mul_cuda(torch.empty((0, 2 * inter), dtype=torch.bfloat16, device="cuda")).shape == (0, inter)
