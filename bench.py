@@ -69,6 +69,9 @@ def parse():
     p.add_argument("--eager", action="store_true", help="no graphs (for profiler attribution)")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-detail", action="store_true", help="headline step only (profiler runs)")
+    p.add_argument("--traffic", metavar="DIR", default=None,
+                   help="write profiles/decode_traffic.json from the four rocprofv3 --pmc runs under DIR "
+                        "(d_FETCH_SIZE, d_WRITE_SIZE: the headline step; c_FETCH_SIZE, c_WRITE_SIZE: --only copy)")
     return p.parse_args()
 
 
@@ -391,8 +394,70 @@ def section_copy(b: Bench):
             "GB/s": round(2 * nbytes / tt / 1e9, 1)}
 
 
+def _pmc_rows(path):
+    import csv
+    import glob
+    files = sorted(glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"bench.py --traffic: no counter_collection.csv under {path}")
+    rows = []
+    for f in files:
+        with open(f) as fh:
+            rows += list(csv.DictReader(fh))
+    return rows
+
+
+def write_traffic(pmc_dir):
+    """Per-launch HBM bytes of the decode kernels from rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (KiB per dispatch), each scaled by what the same counter reads for a plain 256 MiB device
+    copy (bench.py --only copy): bytes = counter KiB x 1024 x (copy bytes / copy counter)."""
+    def mean(name, pick):
+        vals = [float(r["Counter_Value"]) for r in _pmc_rows(os.path.join(pmc_dir, name)) if pick(r["Kernel_Name"])]
+        return sum(vals) / len(vals), len(vals)
+
+    copy = lambda k: "copyBuffer" in k  # noqa: E731
+    dec = lambda k: "decode_rr_kernel" in k or "decode_kernel" in k  # noqa: E731
+    cf, _ = mean("c_FETCH_SIZE", copy)
+    cw, _ = mean("c_WRITE_SIZE", copy)
+    fetch_factor, write_factor = 262144.0 / cf, 262144.0 / cw
+    df, nd = mean("d_FETCH_SIZE", dec)
+    dw, _ = mean("d_WRITE_SIZE", dec)
+    fetch_b = df * 1024 * fetch_factor
+    write_b = dw * 1024 * write_factor
+    algo = sum(w4a16_bytes(m, n, k) for (_, k, n) in SHAPES for m in DECODE_M) / (len(SHAPES) * len(DECODE_M))
+    out = {
+        "kernel": "decode kernels of plm_gemm at M <= 16 (decode_rr_kernel, decode_kernel), Qwen3-8B decode layer "
+                  "set, M in {1,4,16}",
+        "hbm_bytes_per_launch": int(round(fetch_b + write_b)),
+        "algorithmic_bytes_per_launch": int(algo),
+        "ratio": round((fetch_b + write_b) / algo, 4),
+        "fetch_bytes_per_launch": int(round(fetch_b)),
+        "write_bytes_per_launch": int(round(write_b)),
+        "dispatches": nd,
+        "fetch_factor": round(fetch_factor, 4),
+        "write_factor": round(write_factor, 4),
+        "calibration": f"__amd_rocclr_copyBuffer of 256 MiB (python3 bench.py --only copy): FETCH_SIZE {cf:.1f} KiB, "
+                       f"WRITE_SIZE {cw:.1f} KiB per dispatch",
+        "commands": [
+            f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 120 rocprofv3 --pmc {c} -f csv -d "
+            f"/root/repo/{pmc_dir.rstrip('/')}/{p}_{c} -- python3 /root/repo/bench.py {a}"
+            for c in ("FETCH_SIZE", "WRITE_SIZE")
+            for p, a in (("d", "--quick --eager --no-cpu --no-detail"), ("c", "--only copy"))
+        ] + [f"python3 bench.py --traffic {pmc_dir}"],
+        "note": "means over every decode-kernel dispatch of the headline step (12 GEMMs per step, eager, so each "
+                "dispatch is attributed)",
+    }
+    with open(os.path.join(ROOT, "profiles", "decode_traffic.json"), "w") as f:
+        json.dump(out, f, indent=2)
+        f.write("\n")
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
+    if args.traffic:
+        write_traffic(args.traffic)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the hot path is single-GPU)", file=sys.stderr)

@@ -67,6 +67,14 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+def reload_tuning() -> None:
+    """Make the library re-read its PLM_* measurement knobs from the environment (it parses
+    them once per process otherwise). An internal hook for tests, not part of the C ABI."""
+    fn = load().plm_internal_reload_tuning
+    fn.restype, fn.argtypes = None, []
+    fn()
+
+
 def check(rc: int) -> None:
     if rc != PLM_OK:
         msg = load().plm_last_error().decode()

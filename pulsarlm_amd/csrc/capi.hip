@@ -27,13 +27,7 @@ int64_t mfma_workspace_bytes(plm_format f, int64_t m, int64_t n, int64_t k, bool
 // rows except for the widest layer (N = 24576, four or more 16-column strips per CU),
 // where it stops winning above 24 rows. Environment PLM_DECODE_MAX_M (0-32) replaces the
 // rule by a plain threshold, for measuring one path against the other at the same M.
-int64_t decode_env_max_m() {
-    static const int64_t v = [] {
-        const char* e = getenv("PLM_DECODE_MAX_M");
-        return e == nullptr ? int64_t{-1} : std::min<int64_t>(32, std::max<int64_t>(0, atoll(e)));
-    }();
-    return v;
-}
+int64_t decode_env_max_m() { return knobs().decode_max_m; }
 bool use_decode(int64_t m, int64_t n) {
     if (decode_env_max_m() >= 0) return m <= decode_env_max_m();
     if (m <= 16) return true;
@@ -42,8 +36,8 @@ bool use_decode(int64_t m, int64_t n) {
 bool use_decode_w8a8(int64_t m) { return m <= 16 && (decode_env_max_m() < 0 || m <= decode_env_max_m()); }
 
 // Environment PLM_W8A8_UNFUSED: always quantize x in its own launch (A/B measurements and
-// the bit-exactness test of the fused quantizer); read on every call.
-bool fused_quant_off() { return getenv("PLM_W8A8_UNFUSED") != nullptr; }
+// the bit-exactness test of the fused quantizer).
+bool fused_quant_off() { return knobs().w8a8_unfused; }
 
 const char* gemm_op_name(plm_format f) { return f == PLM_INT4 ? "gemm_int4_marlin" : "gemm_fp8_marlin"; }
 
@@ -180,9 +174,13 @@ int plm_gemm_w8a8(const void* x, plm_dtype x_dtype, const void* weight, const vo
 // runs on, held until the process ends. In host code its name is only a stand-in: the
 // device address comes from hipGetSymbolAddress, taken once per device with that device
 // current, and is what the kernels receive. The split-K kernels need the counter region
-// (its first kCounterBytes) zero on entry and leave it zero on exit; set-up clears it once
-// with a fill kernel on the caller's stream (no hipMemsetAsync, so a caller may capture the
-// call). Every call on a GPU shares that GPU's array: calls that overlap on one GPU race.
+// (its first kCounterBytes) zero on entry and leave it zero on exit. The loader zero-fills
+// the array (it has no initializer), and set-up also clears the counter region with a fill
+// kernel on the caller's stream (no hipMemsetAsync, so a caller may capture the call). When
+// that first call is being captured, the fill kernel becomes a node of the caller's graph
+// and re-clears the counters on every replay, which is harmless; the symbol lookup runs in
+// relaxed capture mode so it cannot invalidate the capture. Every call on a GPU shares that
+// GPU's array: calls that overlap on one GPU race.
 // ---------------------------------------------------------------------------
 namespace plm {
 namespace {
@@ -208,7 +206,10 @@ int scratch_of_current_device(const char* op, hipStream_t s, void** out) {
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if (g_scratch[dev] == nullptr) {
         void* p = nullptr;
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        (void)hipThreadExchangeStreamCaptureMode(&mode);
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        (void)hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess || p == nullptr) {
             set_error(op, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
             return PLM_ERR_HIP;

@@ -626,7 +626,7 @@ __global__ void __launch_bounds__(NW * 64, QF ? 8 : 1) decode_rr_kernel(rr_args 
             __syncthreads();
             // Chunk c of a (row, slot) holds K 8c .. 8c + 7 = 32 t + 8 kq + 0..7 with t = c / 4,
             // kq = c % 4; its codes go to byte 32 kq + 8 t of the slot's 128 bytes.
-            const int per_row = 16 << a.nkt_shift;
+            const int per_row = nkt_w * 16;  // only this wavefront's tiles are read back
 #pragma unroll 1
             for (int r = 0; r < (a.m); ++r) {  // wave-uniform
                 const float sc = row_scale(r);
@@ -828,14 +828,10 @@ decode_config choose_decode(plm_format f, int64_t m, int64_t n, int64_t k) {
         c.sp = 1, c.tpw = 2, c.nw = 16;
     }
     if (ktiles < 2 * c.nw) c.nw = ktiles >= 16 ? 8 : 4;
-    if (const char* env = getenv("PLM_DECODE")) {  // "sp,tpw,nw" for tuning sweeps
-        int sp = 0, t = 0, nw = 0;
-        if (sscanf(env, "%d,%d,%d", &sp, &t, &nw) == 3 && (sp == 1 || sp == 2 || sp == 4) && (t == 1 || t == 2) &&
-            (nw == 4 || nw == 8 || nw == 16)) {
-            c.sp = sp;
-            c.tpw = t;
-            c.nw = nw;
-        }
+    if (knobs().decode_sp > 0) {  // PLM_DECODE="sp,tpw,nw" (tuning sweeps)
+        c.sp = knobs().decode_sp;
+        c.tpw = knobs().decode_tpw;
+        c.nw = knobs().decode_nw;
     }
     if (c.sp == 4 && (c.tpw != 1 || c.nw != 16)) c.sp = 2;  // four strips: one instantiation only
     if (c.sp > 1) c.tpw = 1;                                 // two tiles per batch: one strip only
@@ -1012,14 +1008,10 @@ rr_config choose_rr(int64_t m, int64_t n, int64_t k, plm_format f, bool a8) {
             }
         }
     }
-    if (const char* env = getenv("PLM_DECODE_RR")) {  // "sg,nw" for tuning sweeps; "0" disables
-        int sg = 0, nw = 0;
-        const int got = sscanf(env, "%d,%d", &sg, &nw);
-        if (got >= 1 && sg == 0) return rr_config{};
-        if (got == 2 && (sg == 1 || sg == 2 || sg == 3 || sg == 4 || sg == 6) && (nw == 8 || nw == 16)) {
-            c.sg = sg;
-            c.nw = nw;
-        }
+    if (knobs().rr_sg == 0) return rr_config{};  // PLM_DECODE_RR="sg,nw" (tuning sweeps); "0" disables
+    if (knobs().rr_sg > 0) {
+        c.sg = knobs().rr_sg;
+        c.nw = knobs().rr_nw;
     }
     (void)k;
     return c;
@@ -1028,10 +1020,7 @@ rr_config choose_rr(int64_t m, int64_t n, int64_t k, plm_format f, bool a8) {
 // x rows are staged in LDS for M up to this (above it the 16-byte loads of x are mostly full).
 constexpr int64_t kStageMaxM = 4;
 constexpr int64_t kStageMaxBytes = 96 * 1024;  // staging area per workgroup
-bool no_x_staging() {
-    static const bool off = getenv("PLM_DECODE_NO_XS") != nullptr;  // A/B measurements
-    return off;
-}
+bool no_x_staging() { return knobs().decode_no_xs; }  // A/B measurements
 
 int launch_decode(const char* op, plm_format f, const void* x, bool bf16, const void* w, const void* scale,
                   plm_dtype scale_dtype, int64_t m, int64_t n, int64_t k, int64_t block_n, int64_t group_size,

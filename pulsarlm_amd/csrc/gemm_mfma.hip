@@ -563,15 +563,9 @@ struct mfma_config {
     bool tail_halves;
 };
 
-bool tail_halves_off() {
-    static const bool off = getenv("PLM_MFMA_NO_HALVES") != nullptr;  // A/B measurements
-    return off;
-}
+bool tail_halves_off() { return knobs().mfma_no_halves; }  // A/B measurements
 
-bool no_tail() {
-    static const bool off = getenv("PLM_MFMA_NO_TAIL") != nullptr;  // A/B measurements
-    return off;
-}
+bool no_tail() { return knobs().mfma_no_tail; }  // A/B measurements
 
 // Tile shape and split count: the candidate with the least estimated time, counting whole
 // rounds of workgroups over the CUs, a fixed cost of about three K tiles per workgroup
@@ -642,8 +636,8 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
         const double reduce = c.splits > 1 ? 0.5 * c.splits : 0.0;
         return static_cast<double>(rounds) * (c.tiles_per_split + 3 + reduce) * area;
     };
-    if (const char* env = getenv("PLM_MFMA")) {  // tuning sweeps: S, L, H or R
-        const int id = env[0] == 'G' ? 9 : env[0] == 'Q' ? 8 : env[0] == 'E' ? 7 : env[0] == 'X' ? 6 : env[0] == 'H' ? 2 : env[0] == 'L' ? 1 : env[0] == 'R' ? 3 : env[0] == 'T' ? 4 : env[0] == 'W' ? 5 : 0;
+    if (const char f = knobs().mfma_shape) {  // PLM_MFMA (tuning sweeps)
+        const int id = f == 'G' ? 9 : f == 'Q' ? 8 : f == 'E' ? 7 : f == 'X' ? 6 : f == 'H' ? 2 : f == 'L' ? 1 : f == 'R' ? 3 : f == 'T' ? 4 : f == 'W' ? 5 : 0;
         return config(((id == 2 || id == 5) && !wide_ok) || (id == 6 && !tall_ok) || ((id == 7 || id == 8) && !small8_ok) ||
                               (id == 9 && !large8_ok) ? 1 : id);
     }
@@ -876,13 +870,7 @@ int grouped_block_rows(int shape) { return kGroupedShapes[std::min(std::max(shap
 // T = 256 block (16 rows per expert on average, the heaviest experts near 250) 32-row tiles
 // measured 6 % faster than 16-row ones and 64-row ones 5 % slower: a weight tile is
 // dequantized once per row block, and the dequant bounds these small GEMMs.
-int grouped_rows_env() {  // PLM_MOE_ROWS=16/32/64 forces the tile rows (tuning sweeps)
-    static const int v = [] {
-        const char* e = getenv("PLM_MOE_ROWS");
-        return e == nullptr ? 0 : atoi(e);
-    }();
-    return v;
-}
+int grouped_rows_env() { return knobs().moe_rows; }  // PLM_MOE_ROWS=16/32/64 (tuning sweeps)
 int grouped_shape_for(int64_t rows, int64_t n_experts) {
     const int64_t avg = ceil_div(rows, std::max<int64_t>(n_experts, 1));
     switch (grouped_rows_env()) {

@@ -487,13 +487,7 @@ grouped_plan plan_grouped(int64_t rows, int64_t n_experts) {
     return p;
 }
 
-bool small_sort_enabled() {
-    static const bool on = [] {
-        const char* e = getenv("PLM_MOE_SMALL_SORT");  // "0": always the multi-kernel sort (A/B)
-        return e == nullptr || e[0] != '0';
-    }();
-    return on;
-}
+bool small_sort_enabled() { return !knobs().moe_small_sort_off; }  // PLM_MOE_SMALL_SORT=0 (A/B)
 
 int64_t moe_max_tiles(int64_t rows, int64_t n_experts) { return plan_grouped(rows, n_experts).slots(); }
 
@@ -539,10 +533,7 @@ int launch_plan(const char* op, const grouped_plan& p, const void* x, bool bf16,
                           tiles + 3 * p.max_a, p.max_b, tiles + p.count_at() + 1, row_index, p.shape_b, s, swiglu);
 }
 
-bool fused_swiglu_off() {
-    static const bool off = getenv("PLM_MOE_UNFUSED") != nullptr;  // A/B: separate silu_mul launch
-    return off;
-}
+bool fused_swiglu_off() { return knobs().moe_unfused; }  // PLM_MOE_UNFUSED (A/B: separate silu_mul)
 
 }  // namespace
 }  // namespace plm

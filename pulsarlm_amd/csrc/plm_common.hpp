@@ -390,4 +390,23 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 
 int cu_count();
 
+// Measurement knobs: environment variables that force one kernel path against another for
+// A/B timing on the same box (every setting stays within the GEMM tolerance). They are
+// parsed once, at the first call that consults them, so no per-call path reads the
+// environment; plm_internal_reload_tuning() re-parses them (tests only).
+struct tuning {
+    int64_t decode_max_m = -1;         // PLM_DECODE_MAX_M (0-32): plain decode/MFMA threshold
+    bool w8a8_unfused = false;         // PLM_W8A8_UNFUSED: per-token quantizer in its own launch
+    int decode_sp = 0, decode_tpw = 0, decode_nw = 0;  // PLM_DECODE="sp,tpw,nw"
+    int rr_sg = -1, rr_nw = 0;         // PLM_DECODE_RR="sg,nw" (sg 0: round-robin kernel off)
+    bool decode_no_xs = false;         // PLM_DECODE_NO_XS: x from global memory, not LDS
+    char mfma_shape = 0;               // PLM_MFMA=<letter>: force one MFMA tile shape
+    bool mfma_no_halves = false;       // PLM_MFMA_NO_HALVES
+    bool mfma_no_tail = false;         // PLM_MFMA_NO_TAIL
+    int moe_rows = 0;                  // PLM_MOE_ROWS=16/32/64
+    bool moe_small_sort_off = false;   // PLM_MOE_SMALL_SORT=0
+    bool moe_unfused = false;          // PLM_MOE_UNFUSED
+};
+const tuning& knobs();
+
 }  // namespace plm

@@ -4,7 +4,9 @@
 // Counterparts in the reference: repack_weight_kernel / transpose_scale_kernel /
 // repack<> (pulsarlm-core/src/kernels/marlin.cu:197-236,395-445) and its
 // exports repack_int4_marlin_cuda / repack_fp8_marlin_cuda (marlin.cu:601-629).
+#include <algorithm>
 #include <cstdarg>
+#include <cstdlib>
 #include <mutex>
 #include <vector>
 
@@ -40,6 +42,49 @@ int cu_count() {
         counts[dev] = n;
     }
     return counts[dev];
+}
+
+namespace {
+tuning parse_tuning() {
+    tuning t;
+    auto env = [](const char* name) { return getenv(name); };
+    if (const char* e = env("PLM_DECODE_MAX_M")) t.decode_max_m = std::min<int64_t>(32, std::max<int64_t>(0, atoll(e)));
+    t.w8a8_unfused = env("PLM_W8A8_UNFUSED") != nullptr;
+    if (const char* e = env("PLM_DECODE")) {
+        int sp = 0, tp = 0, nw = 0;
+        if (sscanf(e, "%d,%d,%d", &sp, &tp, &nw) == 3 && (sp == 1 || sp == 2 || sp == 4) && (tp == 1 || tp == 2) &&
+            (nw == 4 || nw == 8 || nw == 16))
+            t.decode_sp = sp, t.decode_tpw = tp, t.decode_nw = nw;
+    }
+    if (const char* e = env("PLM_DECODE_RR")) {
+        int sg = 0, nw = 0;
+        const int got = sscanf(e, "%d,%d", &sg, &nw);
+        if (got >= 1 && sg == 0) t.rr_sg = 0;
+        else if (got == 2 && (sg == 1 || sg == 2 || sg == 3 || sg == 4 || sg == 6) && (nw == 8 || nw == 16))
+            t.rr_sg = sg, t.rr_nw = nw;
+    }
+    t.decode_no_xs = env("PLM_DECODE_NO_XS") != nullptr;
+    if (const char* e = env("PLM_MFMA")) t.mfma_shape = e[0];
+    t.mfma_no_halves = env("PLM_MFMA_NO_HALVES") != nullptr;
+    t.mfma_no_tail = env("PLM_MFMA_NO_TAIL") != nullptr;
+    if (const char* e = env("PLM_MOE_ROWS")) t.moe_rows = atoi(e);
+    if (const char* e = env("PLM_MOE_SMALL_SORT")) t.moe_small_sort_off = e[0] == '0';
+    t.moe_unfused = env("PLM_MOE_UNFUSED") != nullptr;
+    return t;
+}
+std::mutex g_tuning_mutex;
+tuning g_tuning;
+bool g_tuning_parsed = false;
+}  // namespace
+
+const tuning& knobs() {
+    static const bool once = [] {
+        std::lock_guard<std::mutex> lock(g_tuning_mutex);
+        if (!g_tuning_parsed) g_tuning = parse_tuning(), g_tuning_parsed = true;
+        return true;
+    }();
+    (void)once;
+    return g_tuning;
 }
 
 namespace {
@@ -98,10 +143,21 @@ __global__ void repack_fp8_kernel(const uint8_t* __restrict__ src, uint32_t* __r
     dst[idx] = word;
 }
 
+// int4 scales whose bf16 rounding reaches 2^120 in magnitude are outside the domain of the
+// GEMM kernels' matrix-core dequant, which forms (128 + u) s in fp32 before subtracting
+// 136 s: at |s| >= 2^120 that product overflows where the reference's round(q round(s))
+// stays finite. The int4 repacks flag such scales (check: 1 = fp32 bits, 2 = bf16 bits).
+__device__ __forceinline__ void flag_scale_domain(uint32_t bits, int check, uint32_t* flag) {
+    if (check == 0) return;
+    const float v = __uint_as_float(check == 1 ? bits : bits << 16);
+    if (fabsf(round_bf16(v)) >= 0x1p120f) atomicOr(flag, 1u);
+}
+
 // Scales [ceil(N/bn), K/g] -> [strips][groups][cols], same element size; padding 0.
 template <typename T>
 __global__ void repack_scale_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t n, int64_t k,
-                                    int64_t block_n, int64_t group_size, int64_t groups, int cols, int64_t total) {
+                                    int64_t block_n, int64_t group_size, int64_t groups, int cols, int64_t total,
+                                    int check, uint32_t* flag) {
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= total) return;
     const int c = static_cast<int>(idx % cols);
@@ -112,6 +168,7 @@ __global__ void repack_scale_kernel(const T* __restrict__ src, T* __restrict__ d
     T v{};
     if (col < n && g < src_groups) v = src[(col / block_n) * src_groups + g];
     dst[idx] = v;
+    flag_scale_domain(static_cast<uint32_t>(v), check, flag);
 }
 
 // Reference Marlin words -> plm int4 words (the mapping of repack_int4_kernel). Marlin
@@ -186,7 +243,7 @@ __global__ void convert_marlin_fp8_kernel(const uint32_t* __restrict__ src, uint
 // scale_marlin fp32 [groups, rows] (marlin.cu:227-236) -> plm fp32 [strips][groups][cols].
 __global__ void convert_marlin_scale_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t n,
                                             int64_t k, int64_t block_n, int64_t group_size, int64_t groups, int cols,
-                                            int64_t total) {
+                                            int64_t total, int check, uint32_t* flag) {
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= total) return;
     const int c = static_cast<int>(idx % cols);
@@ -197,6 +254,7 @@ __global__ void convert_marlin_scale_kernel(const float* __restrict__ src, float
     float v = 0.f;
     if (col < n && g < k / group_size) v = src[g * rows + col / block_n];
     dst[idx] = v;
+    flag_scale_domain(__float_as_uint(v), check, flag);
 }
 
 // Dense W[n, k] = round(q * round(scale)) in the output dtype, from the plm layout.
@@ -242,28 +300,91 @@ int check_common(const char* op, plm_dtype scale_dtype, int64_t n, int64_t k, in
     return PLM_OK;
 }
 
+// The scale-domain flag of the int4 repacks: one word per device in static device memory,
+// addressed through hipGetSymbolAddress, cleared by a fill kernel before each checked repack
+// and read back (with a stream synchronization: repacks run at load time) after it.
+__device__ uint32_t scale_domain_flag;
+std::mutex g_flag_mutex;
+void* g_flag[64];
+
+__global__ void clear_flag_kernel(uint32_t* p) { *p = 0u; }
+
+int scale_flag_of_current_device(const char* op, uint32_t** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_error(op, "no usable current device");
+        return PLM_ERR_HIP;
+    }
+    std::lock_guard<std::mutex> lock(g_flag_mutex);
+    if (g_flag[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scale_domain_flag));
+        if (e != hipSuccess || p == nullptr) {
+            set_error(op, "hipGetSymbolAddress(scale_domain_flag) failed: %s", hipGetErrorString(e));
+            return PLM_ERR_HIP;
+        }
+        g_flag[dev] = p;
+    }
+    *out = static_cast<uint32_t*>(g_flag[dev]);
+    return PLM_OK;
+}
+
+// After a checked int4 scale repack was queued on `stream`: wait for it and reject the
+// weights if a scale fell outside the kernels' domain.
+int read_scale_flag(const char* op, uint32_t* flag, hipStream_t stream) {
+    uint32_t host = 0;
+    if (hipMemcpyAsync(&host, flag, sizeof(host), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+        hipStreamSynchronize(stream) != hipSuccess) {
+        set_error(op, "reading the scale check failed: %s", hipGetErrorString(hipGetLastError()));
+        return PLM_ERR_HIP;
+    }
+    PLM_CHECK_ARG(host == 0, op,
+                  "int4 scales must be below 2^120 in magnitude after rounding to bf16 (the GEMM kernels form "
+                  "(128 + q + 8) * scale in fp32)");
+    return PLM_OK;
+}
+
 int launch_scale_repack(const char* op, const void* src, plm_dtype dt, int64_t n, int64_t k, int64_t block_n,
-                        int64_t group_size, void* dst, hipStream_t stream) {
+                        int64_t group_size, void* dst, hipStream_t stream, bool int4) {
     const layout_dims d = make_dims(n, k, block_n, group_size);
     const int64_t total = d.strips * d.groups * d.scale_cols;
     if (total == 0) return PLM_OK;
+    // fp16 scales are below 65520 in magnitude: only fp32 and bf16 int4 scales are checked.
+    const int check = !int4 ? 0 : dt == PLM_FP32 ? 1 : dt == PLM_BF16 ? 2 : 0;
+    uint32_t* flag = nullptr;
+    if (check != 0) {
+        if (int rc = scale_flag_of_current_device(op, &flag)) return rc;
+        clear_flag_kernel<<<1, 1, 0, stream>>>(flag);
+        PLM_HIP_LAUNCH_CHECK(op);
+    }
     if (dt == PLM_FP32) {
         repack_scale_kernel<uint32_t><<<blocks_for(total), kThreads, 0, stream>>>(
             static_cast<const uint32_t*>(src), static_cast<uint32_t*>(dst), n, k, block_n, group_size, d.groups,
-            d.scale_cols, total);
+            d.scale_cols, total, check, flag);
     } else {
         repack_scale_kernel<uint16_t><<<blocks_for(total), kThreads, 0, stream>>>(
             static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), n, k, block_n, group_size, d.groups,
-            d.scale_cols, total);
+            d.scale_cols, total, check, flag);
     }
     PLM_HIP_LAUNCH_CHECK(op);
-    return PLM_OK;
+    return check != 0 ? read_scale_flag(op, flag, stream) : PLM_OK;
 }
 
 }  // namespace
 }  // namespace plm
 
 using namespace plm;
+
+extern "C" {
+// Not part of the public ABI (include/pulsarlm_amd.h): re-reads the measurement knobs from the
+// environment, so a test can select one path and then the other within one process. Not
+// thread-safe against concurrent GEMM calls.
+__attribute__((visibility("default"))) void plm_internal_reload_tuning() {
+    std::lock_guard<std::mutex> lock(plm::g_tuning_mutex);
+    plm::g_tuning = plm::parse_tuning();
+    plm::g_tuning_parsed = true;
+}
+}  // extern "C"
 
 extern "C" {
 
@@ -299,7 +420,7 @@ int plm_repack_int4(const int32_t* weight_packed, const void* weight_scale, plm_
                                                                   n, k, ceil_div(k, kTileK), total);
         PLM_HIP_LAUNCH_CHECK(op);
     }
-    return launch_scale_repack(op, weight_scale, scale_dtype, n, k, block_n, group_size, scale_out, s);
+    return launch_scale_repack(op, weight_scale, scale_dtype, n, k, block_n, group_size, scale_out, s, true);
 }
 
 int plm_repack_fp8(const uint8_t* weight, const void* weight_scale, plm_dtype scale_dtype, int64_t n, int64_t k,
@@ -316,7 +437,7 @@ int plm_repack_fp8(const uint8_t* weight, const void* weight_scale, plm_dtype sc
                                                                  ceil_div(k, kTileK), total);
         PLM_HIP_LAUNCH_CHECK(op);
     }
-    return launch_scale_repack(op, weight_scale, scale_dtype, n, k, block_n, group_size, scale_out, s);
+    return launch_scale_repack(op, weight_scale, scale_dtype, n, k, block_n, group_size, scale_out, s, false);
 }
 
 int plm_convert_marlin(plm_format format, const int32_t* weight_marlin, const float* scale_marlin, int64_t n,
@@ -345,9 +466,18 @@ int plm_convert_marlin(plm_format format, const int32_t* weight_marlin, const fl
     const layout_dims d = make_dims(n, k, block_n, group_size);
     const int64_t stotal = d.strips * d.groups * d.scale_cols;
     if (stotal > 0) {
+        const int check = format == PLM_INT4 ? 1 : 0;
+        uint32_t* flag = nullptr;
+        if (check != 0) {
+            if (int rc = scale_flag_of_current_device(op, &flag)) return rc;
+            clear_flag_kernel<<<1, 1, 0, s>>>(flag);
+            PLM_HIP_LAUNCH_CHECK(op);
+        }
         convert_marlin_scale_kernel<<<blocks_for(stotal), kThreads, 0, s>>>(
-            scale_marlin, static_cast<float*>(scale_out), n, k, block_n, group_size, d.groups, d.scale_cols, stotal);
+            scale_marlin, static_cast<float*>(scale_out), n, k, block_n, group_size, d.groups, d.scale_cols, stotal,
+            check, flag);
         PLM_HIP_LAUNCH_CHECK(op);
+        if (check != 0) return read_scale_flag(op, flag, s);
     }
     return PLM_OK;
 }

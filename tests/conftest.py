@@ -24,3 +24,22 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture
+def tuning_env(monkeypatch):
+    """Set or clear one of the library's measurement knobs (PLM_* environment variables),
+    which it parses once per process, and make it re-read them; on teardown the
+    environment is restored and re-read again."""
+    from pulsarlm_amd import _lib
+
+    def set_knob(name, value):
+        if value is None:
+            monkeypatch.delenv(name, raising=False)
+        else:
+            monkeypatch.setenv(name, value)
+        _lib.reload_tuning()
+
+    yield set_knob
+    monkeypatch.undo()
+    _lib.reload_tuning()

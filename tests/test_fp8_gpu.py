@@ -147,7 +147,7 @@ _FUSED_CASES = ([(m, 5120, 5120, *c) for m in (1, 2, 3, 4) for c in _FUSED_SCALE
 
 
 @pytest.mark.parametrize("m,k,n,block_n,sdt,dtype", _FUSED_CASES)
-def test_w8a8_fused_quantizer_bit_exact(m, k, n, block_n, sdt, dtype, monkeypatch):
+def test_w8a8_fused_quantizer_bit_exact(m, k, n, block_n, sdt, dtype, tuning_env):
     """W8A8 at M <= 4 quantizes x inside the GEMM kernel when each wavefront of the
     workgroup holds one to three K tiles: 16 wavefronts at K = 5120 and 4992 (40 and 39
     tiles; N = 34816 too, where the unfused kernel takes 8), 8 at N = 16384 (16 tiles).
@@ -176,9 +176,9 @@ def test_w8a8_fused_quantizer_bit_exact(m, k, n, block_n, sdt, dtype, monkeypatc
     x = O.round_to(x, dtype)
     xd = to_dev(x, TDT[dtype])
     fused = ops.gemm_fp8_w8a8_cuda(xd, wt, st, n, block_n, 128)
-    monkeypatch.setenv("PLM_W8A8_UNFUSED", "1")
+    tuning_env("PLM_W8A8_UNFUSED", "1")
     split = ops.gemm_fp8_w8a8_cuda(xd, wt, st, n, block_n, 128)
-    monkeypatch.delenv("PLM_W8A8_UNFUSED")
+    tuning_env("PLM_W8A8_UNFUSED", None)
     torch.cuda.synchronize()
     # N = 34816: the fused kernel runs 16 wavefronts and the unfused one 8, so the
     # wavefronts' partial sums are added in another order; both are held to the bound below.

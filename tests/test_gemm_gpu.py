@@ -345,14 +345,14 @@ def test_full_size_against_gpu_fp32(shape, m):
 
 @pytest.mark.parametrize("n", [1024, 1000, 1004])
 @pytest.mark.parametrize("y_shift", [0, 1])
-def test_mfma_epilogue_store_forms(n, y_shift, monkeypatch):
+def test_mfma_epilogue_store_forms(n, y_shift, tuning_env):
     """The tall shape stores its output 16 bytes at a time when N % 8 == 0 and y is 16-byte
     aligned, and element by element otherwise (y need only be 2-byte aligned; N = 1004 and a
     y one element past an aligned address take the fallback). Both forms must give the
     aligned call's result on the same shape bit for bit, and every row must match the fp32
     reference."""
     m, k = 512, 512  # 8 tall tiles, K not split (the split-K kernels keep the 2-byte stores)
-    monkeypatch.setenv("PLM_MFMA", "X")
+    tuning_env("PLM_MFMA", "X")
     x, packed, s = _full_case(m, k, n, seed=n + y_shift)
     w, sc = ops.repack_int4_marlin_cuda(packed, s, 1, 128)
     wd = ops.dequant_marlin_cuda("int4", w, sc, n, k, 1, 128)
@@ -438,3 +438,49 @@ def test_decode_long_k(m, n, k, g, dtype):
     x = x_case(m, k, dtype, seed=m + 3)
     y = ops.gemm_int4_marlin_cuda(to_dev(x, TDT[dtype]), w, sc, n, 1, g)
     assert_close(y, O.gemm_ref(x, O.dequant_int4(packed, s, 1, g, dtype), None), f"m={m} n={n} k={k} g={g}")
+
+
+# ------------------------------------------------------------------ int4 scale domain
+
+
+def _edge_scales(n, groups, seed):
+    """bf16-exact scales in [2^119, 2^120): the largest the int4 kernels accept."""
+    j = np.random.default_rng(seed).integers(0, 128, size=(n, groups))
+    return (np.ldexp(1.0 + j / 128.0, 119)).astype(np.float32)
+
+
+@pytest.mark.parametrize("m", [1, 16, 256])
+@pytest.mark.parametrize("sdt", ["fp32", "bf16"])
+def test_int4_scale_domain_edge_exact(m, sdt):
+    """Scales just below 2^120 (where (128 + q + 8) s still fits fp32) go through the decode
+    (M = 1, 16) and MFMA (M = 256) kernels exactly: the identity rows of x pick out
+    round(q round(s)) bit for bit, as test_marlin.cpp:54-78 does for ordinary scales."""
+    n, k, g = 64, 256, 128
+    print(f"scale edge m={m} scale={sdt}", flush=True)
+    packed, _ = int4_case(n, k, g, 1, seed=m)
+    s = _edge_scales(n, k // g, seed=m)
+    st = to_dev(s) if sdt == "fp32" else to_dev(s, torch.bfloat16)
+    w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), st, 1, g)
+    cols = np.random.default_rng(m + 1).permutation(k)[:m]
+    x = np.zeros((m, k), np.float32)
+    x[np.arange(m), cols] = 1.0
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, torch.bfloat16), w, sc, n, 1, g)
+    ref = O.dequant_int4(packed, s, 1, g, "bf16")[:, cols].T
+    got = to_np(y)
+    assert np.isfinite(got).all()
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("sdt", ["fp32", "bf16"])
+def test_int4_scales_beyond_the_domain_are_rejected(sdt):
+    """A scale whose bf16 rounding reaches 2^120 is refused at repack time with the op's
+    name (the kernels would overflow (128 + q + 8) s), and so is one that rounds up to it;
+    one bf16 step below passes (previous test)."""
+    n, k, g = 32, 256, 128
+    packed, _ = int4_case(n, k, g, 1, seed=7)
+    for big in (2.0**120, np.float32(2.0**120 * (1 - 2.0**-10))):  # the second rounds up to 2^120 in bf16
+        s = np.full((n, k // g), 0.02, np.float32)
+        s[5, 1] = -big
+        st = to_dev(s) if sdt == "fp32" else to_dev(s, torch.bfloat16)
+        with pytest.raises(Exception, match=r"repack_int4_marlin: int4 scales must be below 2\^120"):
+            ops.repack_int4_marlin_cuda(to_dev(packed), st, 1, g)
