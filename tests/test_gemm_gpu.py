@@ -484,3 +484,27 @@ def test_int4_scales_beyond_the_domain_are_rejected(sdt):
         st = to_dev(s) if sdt == "fp32" else to_dev(s, torch.bfloat16)
         with pytest.raises(Exception, match=r"repack_int4_marlin: int4 scales must be below 2\^120"):
             ops.repack_int4_marlin_cuda(to_dev(packed), st, 1, g)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 6144), (4, 4096, 24576), (1, 12288, 512), (3, 12288, 512)])
+def test_int4_scales_across_ranges_exact(m, k, n):
+    """Scales mostly ordinary, with scattered groups below 2^-17 or at 2^16 and above, and one
+    strip entirely at 2^-18, through the decode kernels (round-robin at K = 4096, split-K at
+    K = 12288): identity rows of x must pick out round(q round(s)) bit for bit in every
+    column."""
+    g = 128
+    print(f"scale ranges m={m} k={k} n={n}", flush=True)
+    rng = np.random.default_rng(k + n + m)
+    packed, s = int4_case(n, k, g, 1, seed=m + 3, scale_dtype=np.float32)
+    groups = s.shape[1]
+    pick = rng.random(s.shape) < 0.01
+    s[pick] = rng.choice(np.array([3.0e-6, 1.5e-7, 7.0e4, -1.2e5, 2.0**-17, 2.0**16], np.float32), pick.sum())
+    s[0, :] = 2.0**-18  # one strip entirely on the bf16 form
+    w, sc = ops.repack_int4_marlin_cuda(to_dev(packed), to_dev(s), 1, g)
+    cols = rng.permutation(k)[:m]
+    x = np.zeros((m, k), np.float32)
+    x[np.arange(m), cols] = 1.0
+    y = ops.gemm_int4_marlin_cuda(to_dev(x, torch.bfloat16), w, sc, n, 1, g)
+    ref = O.dequant_int4(packed, s, 1, g, "bf16")[:, cols].T
+    assert np.array_equal(to_np(y), ref)
+    assert groups == k // g
