@@ -258,7 +258,24 @@ def section_decode(b: Bench, steps, warmup, detail_shapes=True):
     }
 
 
+def mfma_plan(b: Bench, m, n, k, fmt=None, a8=False):
+    """The MFMA kernel's decomposition of a plain GEMM (an internal hook of the library)."""
+    import ctypes
+    fn = b.lib.plm_internal_mfma_plan
+    fn.restype, fn.argtypes = None, [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                     ctypes.POINTER(ctypes.c_int32)]
+    out = (ctypes.c_int32 * 8)()
+    fn(b._lib.PLM_INT4 if fmt is None else fmt, m, n, k, int(a8), out)
+    return {"tile": f"{out[0]}x{out[1]}", "tiles": out[2], "k_splits": out[3], "tail_tiles": out[4],
+            "tail": "128-row halves" if out[6] else (f"K split {out[5]} ways" if out[4] else None),
+            "skip_reduction_build": bool(out[7])}
+
+
 def section_prefill(b: Bench):
+    """Config 3. Cases whose plan splits K across workgroups or runs a tail launch (the
+    split-K / stream-K-style decomposition) are also timed with PLM_MFMA_UNSPLIT (whole tiles,
+    no K split, no tail) as `unsplit_us`, so the decomposition's net effect is measured live;
+    the reduction's own cost is measured with a PLM_MEASURE_SKIP_REDUCTION build."""
     torch, L = b.torch, b._lib
     out = {}
     tot_flop = tot_t = 0.0
@@ -272,9 +289,20 @@ def section_prefill(b: Bench):
             tf = 2 * m * n * k / tt / 1e12
             tot_flop += 2 * m * n * k
             tot_t += tt
-            out[f"{name}_m{m}"] = {"us": round(tt * 1e6, 1), "TFLOP/s": round(tf, 1),
-                                   "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 3)}
+            plan = mfma_plan(b, m, n, k)
+            rec = {"us": round(tt * 1e6, 1), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 3),
+                   "plan": {key: v for key, v in plan.items() if key != "skip_reduction_build"}}
+            if plan["k_splits"] > 1 or plan["tail_tiles"]:
+                os.environ["PLM_MFMA_UNSPLIT"] = "1"
+                L.reload_tuning()
+                tu = b.time(launches, reps=2 if m == 4096 else 4) / len(copies)
+                del os.environ["PLM_MFMA_UNSPLIT"]
+                L.reload_tuning()
+                rec["unsplit_us"] = round(tu * 1e6, 1)
+            out[f"{name}_m{m}"] = rec
         del copies
+    if mfma_plan(b, 256, 4096, 4096)["skip_reduction_build"]:
+        out["measurement_build"] = "PLM_MEASURE_SKIP_REDUCTION: split-K reductions skipped, results invalid"
     out["aggregate_TFLOP/s"] = round(tot_flop / tot_t / 1e12, 1)
     out["vendor_bf16_reference"] = vendor_bf16_reference(b)
     return out
@@ -475,6 +503,10 @@ def main():
         print(json.dumps({args.only: fn(b)}))
         return
 
+    if mfma_plan(b, 256, 4096, 4096)["skip_reduction_build"]:
+        print("bench.py: this library is a PLM_MEASURE_SKIP_REDUCTION measurement build (invalid results); "
+              "only --only prefill runs on it", file=sys.stderr)
+        sys.exit(2)
     d = section_decode(b, args.steps, args.warmup, detail_shapes=not args.no_detail)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "decode_traffic.json")

@@ -2,7 +2,9 @@
 C++ host layer ``_host.so`` (pulsarlm-core's operator signatures over the C ABI,
 bound for Python) with g++ against PyTorch-ROCm.
 
-Usage: ``python -m pulsarlm_amd.build`` (or ``__graft_entry__.build()``).
+Usage: ``python -m pulsarlm_amd.build [-DNAME=VALUE ...]`` (or ``__graft_entry__.build()``);
+extra ``-D`` definitions go to every hipcc compile (measurement builds such as
+``-DPLM_MEASURE_SKIP_REDUCTION=1``, whose results are invalid by design).
 Every call recompiles; objects go to ``pulsarlm_amd/_build/`` and are linked
 in parallel-compiled order into ``pulsarlm_amd/libpulsarlm_amd.so``.
 """
@@ -43,11 +45,14 @@ FLAGS = [
 SOURCE_FLAGS = {"gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
+EXTRA_DEFINES: list[str] = []
+
+
 def _compile(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
     # The compiler's per-kernel resource report (registers, LDS, scratch) is kept next to
     # the object: tests/test_build.py checks that no kernel spills to scratch.
-    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-Rpass-analysis=kernel-resource-usage", "-c",
+    cmd = [HIPCC, *FLAGS, *EXTRA_DEFINES, *SOURCE_FLAGS.get(src, []), "-Rpass-analysis=kernel-resource-usage", "-c",
            str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -120,5 +125,6 @@ def build(verbose: bool = False) -> Path:
 
 
 if __name__ == "__main__":
+    EXTRA_DEFINES.extend(a for a in sys.argv[1:] if a.startswith("-D"))
     build(verbose=True)
     sys.exit(0)

@@ -421,7 +421,13 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     // MFMA tile, so each store instruction is one contiguous 1 KiB) into its own slot of the
     // work tile's partial area; the last workgroup to arrive reloads all slots and sums them
     // in split order, so the result does not depend on arrival order.
-    if (a.splits > 1) {
+    // PLM_MEASURE_SKIP_REDUCTION (a measurement build only, never the shipped library): the
+    // split workgroups write their own partial sums as the result, so timing the same launches
+    // with and without it gives the cost of the split-K reduction (wrong results).
+#ifndef PLM_MEASURE_SKIP_REDUCTION
+#define PLM_MEASURE_SKIP_REDUCTION 0
+#endif
+    if (a.splits > 1 && !PLM_MEASURE_SKIP_REDUCTION) {
         constexpr int TILE_BYTES = MT * NS * NT * 16;
         const __amdgpu_buffer_rsrc_t p_rsrc = make_rsrc(
             reinterpret_cast<uint8_t*>(a.partial) + static_cast<int64_t>(blockIdx.x) * a.splits * TILE_BYTES,
@@ -581,7 +587,7 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
     const bool large8_ok = f == PLM_FP8 && !a8;
     const int64_t cus = cu_count();
     const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
-    auto config = [&](int id) {
+    auto config = [&](int id, bool split_ok = true) {
         const shape sh = shape_of(id);
         mfma_config c{};
         c.shape = id;
@@ -589,13 +595,13 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
         c.n_blocks = static_cast<int>(ceil_div(strips, sh.bs()));
         const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
         int64_t splits = 1;
-        if (tiles < cus && tiles <= kMaxCounters)
+        if (tiles < cus && tiles <= kMaxCounters && !knobs().mfma_unsplit && split_ok)
             splits = std::max<int64_t>(1, std::min<int64_t>(ceil_div(cus, tiles), ktiles / 4));
         c.tiles_per_split = static_cast<int>(ceil_div(ktiles, splits));
         c.splits = static_cast<int>(ceil_div(ktiles, c.tiles_per_split));
         const int64_t rem = tiles % cus;
         if (c.splits == 1 && tiles > cus && rem > 0 && 2 * rem <= cus && rem <= kMaxCounters && ktiles >= 8 &&
-            !no_tail()) {
+            !no_tail() && !knobs().mfma_unsplit) {
             const int64_t ts = std::min<int64_t>(cus / rem, ktiles / 4);
             c.tail_tiles_per_split = static_cast<int>(ceil_div(ktiles, ts));
             c.tail_splits = static_cast<int>(ceil_div(ktiles, c.tail_tiles_per_split));
@@ -609,6 +615,11 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
             }
         }
         return c;
+    };
+    auto unsplit_partial = [&](const mfma_config& c) {
+        const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
+        return f == PLM_INT4 && !a8 && shape_of(c.shape).bm() >= 256 && c.splits == 1 && 2 * tiles >= cus &&
+               tiles < cus;
     };
     auto cost = [&](const mfma_config& c) {
         const shape sh = shape_of(c.shape);
@@ -631,6 +642,11 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
             return (static_cast<double>(full_rounds) * (c.tiles_per_split + 3) + c.tail_tiles_per_split + 3 +
                     0.5 * c.tail_splits) * area;
         }
+        // int4 W4A16, 256-row tiles filling half the CUs or more without a K split: the busy
+        // CUs run each K step faster than in a full round (measured on MI355X at the Qwen3-8B
+        // shapes, M = 256 and 1024: a K step of 256 x 192 took 2.0 us with 128 workgroups
+        // against 3.65 us with 256), so the round counts in proportion to the CUs used.
+        if (unsplit_partial(c)) return static_cast<double>(tiles) / cus * (ktiles + 3) * area;
         const int64_t rounds = ceil_div(tiles * c.splits, cus);
         // The last workgroup of a split tile reads every split's partials: half a K tile each.
         const double reduce = c.splits > 1 ? 0.5 * c.splits : 0.0;
@@ -648,6 +664,8 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
             continue;
         const mfma_config c = config(id);
         if (cost(c) < cost(best)) best = c;
+        const mfma_config u = config(id, false);  // the same tiles without a K split
+        if (unsplit_partial(u) && cost(u) < cost(best)) best = u;
     }
     return best;
 }
@@ -929,3 +947,24 @@ int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const
 }
 
 }  // namespace plm
+
+extern "C" {
+// Not part of the public ABI (include/pulsarlm_amd.h): the MFMA kernel's plan for a plain GEMM,
+// for bench.py's report of the split-K / tail decomposition. out[0..7]: tile rows, tile
+// columns, work tiles, K splits, tail tiles, tail K splits, tail as 128-row halves (0/1), and
+// whether this build skips the split-K reduction (a measurement build, results invalid).
+__attribute__((visibility("default"))) void plm_internal_mfma_plan(int format, int64_t m, int64_t n, int64_t k, int a8,
+                                                                  int32_t* out) {
+    using namespace plm;
+    const mfma_config c = choose_mfma(static_cast<plm_format>(format), m, n, k, a8 != 0);
+    const shape sh = shape_of(c.shape);
+    out[0] = sh.bm();
+    out[1] = sh.bs() * kTileN;
+    out[2] = c.m_blocks * c.n_blocks;
+    out[3] = c.splits;
+    out[4] = c.tail_tiles;
+    out[5] = c.tail_halves ? 1 : c.tail_splits;
+    out[6] = c.tail_halves ? 1 : 0;
+    out[7] = PLM_MEASURE_SKIP_REDUCTION;
+}
+}  // extern "C"

@@ -403,6 +403,7 @@ struct tuning {
     char mfma_shape = 0;               // PLM_MFMA=<letter>: force one MFMA tile shape
     bool mfma_no_halves = false;       // PLM_MFMA_NO_HALVES
     bool mfma_no_tail = false;         // PLM_MFMA_NO_TAIL
+    bool mfma_unsplit = false;         // PLM_MFMA_UNSPLIT: no K split and no tail launch
     int moe_rows = 0;                  // PLM_MOE_ROWS=16/32/64
     bool moe_small_sort_off = false;   // PLM_MOE_SMALL_SORT=0
     bool moe_unfused = false;          // PLM_MOE_UNFUSED

@@ -67,6 +67,7 @@ tuning parse_tuning() {
     if (const char* e = env("PLM_MFMA")) t.mfma_shape = e[0];
     t.mfma_no_halves = env("PLM_MFMA_NO_HALVES") != nullptr;
     t.mfma_no_tail = env("PLM_MFMA_NO_TAIL") != nullptr;
+    t.mfma_unsplit = env("PLM_MFMA_UNSPLIT") != nullptr;
     if (const char* e = env("PLM_MOE_ROWS")) t.moe_rows = atoi(e);
     if (const char* e = env("PLM_MOE_SMALL_SORT")) t.moe_small_sort_off = e[0] == '0';
     t.moe_unfused = env("PLM_MOE_UNFUSED") != nullptr;
