@@ -273,9 +273,10 @@ def mfma_plan(b: Bench, m, n, k, fmt=None, a8=False):
 
 def section_prefill(b: Bench):
     """Config 3. Cases whose plan splits K across workgroups or runs a tail launch (the
-    split-K / stream-K-style decomposition) are also timed with PLM_MFMA_UNSPLIT (whole tiles,
-    no K split, no tail) as `unsplit_us`, so the decomposition's net effect is measured live;
-    the reduction's own cost is measured with a PLM_MEASURE_SKIP_REDUCTION build."""
+    split-K / stream-K-style decomposition) are also timed under PLM_MFMA_UNSPLIT, which takes
+    the best plan with whole-K tiles and no tail launch (`no_split_us`, its plan in
+    `no_split_plan`), so what the decomposition buys is measured live; the reduction's own
+    cost is measured with a PLM_MEASURE_SKIP_REDUCTION build."""
     torch, L = b.torch, b._lib
     out = {}
     tot_flop = tot_t = 0.0
@@ -296,9 +297,11 @@ def section_prefill(b: Bench):
                 os.environ["PLM_MFMA_UNSPLIT"] = "1"
                 L.reload_tuning()
                 tu = b.time(launches, reps=2 if m == 4096 else 4) / len(copies)
+                up = mfma_plan(b, m, n, k)
                 del os.environ["PLM_MFMA_UNSPLIT"]
                 L.reload_tuning()
-                rec["unsplit_us"] = round(tu * 1e6, 1)
+                rec["no_split_us"] = round(tu * 1e6, 1)
+                rec["no_split_plan"] = f"{up['tile']} x{up['tiles']}"
             out[f"{name}_m{m}"] = rec
         del copies
     if mfma_plan(b, 256, 4096, 4096)["skip_reduction_build"]:

@@ -587,7 +587,7 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
     const bool large8_ok = f == PLM_FP8 && !a8;
     const int64_t cus = cu_count();
     const int64_t strips = ceil_div(n, kTileN), ktiles = ceil_div(k, kTileK);
-    auto config = [&](int id, bool split_ok = true) {
+    auto config = [&](int id) {
         const shape sh = shape_of(id);
         mfma_config c{};
         c.shape = id;
@@ -595,7 +595,7 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
         c.n_blocks = static_cast<int>(ceil_div(strips, sh.bs()));
         const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
         int64_t splits = 1;
-        if (tiles < cus && tiles <= kMaxCounters && !knobs().mfma_unsplit && split_ok)
+        if (tiles < cus && tiles <= kMaxCounters && !knobs().mfma_unsplit)
             splits = std::max<int64_t>(1, std::min<int64_t>(ceil_div(cus, tiles), ktiles / 4));
         c.tiles_per_split = static_cast<int>(ceil_div(ktiles, splits));
         c.splits = static_cast<int>(ceil_div(ktiles, c.tiles_per_split));
@@ -615,11 +615,6 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
             }
         }
         return c;
-    };
-    auto unsplit_partial = [&](const mfma_config& c) {
-        const int64_t tiles = static_cast<int64_t>(c.m_blocks) * c.n_blocks;
-        return f == PLM_INT4 && !a8 && shape_of(c.shape).bm() >= 256 && c.splits == 1 && 2 * tiles >= cus &&
-               tiles < cus;
     };
     auto cost = [&](const mfma_config& c) {
         const shape sh = shape_of(c.shape);
@@ -642,11 +637,6 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
             return (static_cast<double>(full_rounds) * (c.tiles_per_split + 3) + c.tail_tiles_per_split + 3 +
                     0.5 * c.tail_splits) * area;
         }
-        // int4 W4A16, 256-row tiles filling half the CUs or more without a K split: the busy
-        // CUs run each K step faster than in a full round (measured on MI355X at the Qwen3-8B
-        // shapes, M = 256 and 1024: a K step of 256 x 192 took 2.0 us with 128 workgroups
-        // against 3.65 us with 256), so the round counts in proportion to the CUs used.
-        if (unsplit_partial(c)) return static_cast<double>(tiles) / cus * (ktiles + 3) * area;
         const int64_t rounds = ceil_div(tiles * c.splits, cus);
         // The last workgroup of a split tile reads every split's partials: half a K tile each.
         const double reduce = c.splits > 1 ? 0.5 * c.splits : 0.0;
@@ -664,8 +654,6 @@ mfma_config choose_mfma(plm_format f, int64_t m, int64_t n, int64_t k, bool a8) 
             continue;
         const mfma_config c = config(id);
         if (cost(c) < cost(best)) best = c;
-        const mfma_config u = config(id, false);  // the same tiles without a K split
-        if (unsplit_partial(u) && cost(u) < cost(best)) best = u;
     }
     return best;
 }
