@@ -80,7 +80,7 @@ template <bool A8> struct a_traits {
 
 // VO: the 16-byte epilogue (see its comment) is compiled in; the host selects it per launch.
 template <plm_format F, bool BF16, bool UNIFORM, bool WIDE, bool A8, bool GROUPED, int WM, int WN, int MT, int NS,
-          bool VO = false>
+          bool VO = false, bool PERSIST = false>
 __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     constexpr int NW = WM * WN;  // wavefronts
     constexpr int NT = NW * 64;
@@ -108,7 +108,8 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     constexpr bool PIPE_A = UNIFORM && !A8 && WM == 1 && MT >= 8;
     // Fragments kept a slice ahead: all MT, or 12 for fp8, whose weight tiles already hold
     // two K steps of registers (16 would spill).
-    constexpr int PD = F == PLM_FP8 ? MT - 4 : MT;
+    // PERSIST keeps 8 fewer: the item loop needs the registers (the tall tile spills otherwise).
+    constexpr int PD = F == PLM_FP8 ? MT - 4 : (PERSIST ? MT - 8 : MT);
 
     // Two stages of [A tile | weight tiles]. Stage s holds K step kt_begin + s (mod 2); the
     // loads of step kt + 1 go straight from HBM into the other stage while step kt computes.
@@ -123,406 +124,468 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
     const int wm = wave / WN, wn = wave % WN;
     const int col16 = lane & 15, kq = lane >> 4;
     const int split = blockIdx.y;
+    const bool swiglu = GROUPED && a.swiglu_strips > 0;
+    const int kt_begin = split * a.tiles_per_split;
+    const int kt_end = min(kt_begin + a.tiles_per_split, a.ktiles);
+    const int a_stride = A8 ? a.ktiles * kTileK : a.k * 2;
+    const int strip_bytes = a.ktiles * TB;
+    const bool bf16_scale = a.scale_dtype == PLM_BF16;
+    const int s_row = a.groups * a.scale_cols * ES;  // scale bytes per strip
+    const int s_lane = a.scale_cols == 1 ? 0 : col16 * ES;
+    const int lrow = lane / SLOTS, lslot = lane % SLOTS;
 
-    // Work tile: (row block, column block), grouped: (expert tile, column block).
-    int nb, expert = 0, row0, rows;
+    // Work items: plain calls take work tile blockIdx.x + tile_base (row block fastest);
+    // grouped calls take (expert tile, column block) items. Workgroups are dealt to the 8
+    // XCDs round-robin by id, so a grouped call gives out its real items in 8 contiguous runs,
+    // one per XCD: the column blocks of a row tile (the same x rows) and the consecutive
+    // tiles of an expert (the same weights) run on one XCD and share its L2; ids past the
+    // real items exit. PERSIST (grouped only; an A/B option, measured slower than one item
+    // per workgroup): the grid holds about one workgroup per slot the CUs keep resident, each
+    // workgroup walks its XCD's run gridDim.x / 8 items apart and loads the next item's first
+    // K step into the free LDS stage during the current item's epilogue.
+    static_assert(!PERSIST || (GROUPED && !A8), "persistent launches are grouped ones");
+    int items = 0, per_xcd = 0;
     if constexpr (GROUPED) {
-        // Workgroups are dealt to the 8 XCDs round-robin by id. The real (tile, column
-        // block) items are given out in 8 contiguous runs, one per XCD, so the column
-        // blocks of a row tile (the same x rows) and the consecutive tiles of an expert
-        // (the same weights) run on one XCD and share its L2; ids past the real items exit.
-        const int items = uniform(*a.tile_count) * a.n_blocks;
-        const int per_xcd = (items + 7) >> 3;
-        const int idx = blockIdx.x >> 3;
-        if (idx >= per_xcd) return;
-        const int item = (blockIdx.x & 7) * per_xcd + idx;
-        if (item >= items) return;
-        const int tile = item / a.n_blocks;
-        nb = item % a.n_blocks;
-        expert = a.tiles[3 * tile];
-        row0 = a.tiles[3 * tile + 1];
-        rows = a.tiles[3 * tile + 2];
-        if (rows <= 0) return;  // uniform across the workgroup
-    } else {
-        const int tile = blockIdx.x + a.tile_base;
-        const int mb = tile % a.m_blocks;
-        nb = tile / a.m_blocks;
-        row0 = mb * BM;
-        rows = min(BM, a.m - row0);
+        items = uniform(*a.tile_count) * a.n_blocks;
+        per_xcd = (items + 7) >> 3;
     }
-    const int strip0 = nb * BS;
+    auto item_at = [&](int pos) -> int {  // this workgroup's pos-th item, -1 past its last
+        if constexpr (GROUPED) {
+            const int idx = (blockIdx.x >> 3) + pos * (gridDim.x >> 3);
+            if (idx >= per_xcd) return -1;
+            const int it = (blockIdx.x & 7) * per_xcd + idx;
+            return it < items ? it : -1;
+        } else {
+            return blockIdx.x + a.tile_base;
+        }
+    };
+
+    // Everything that depends on the item: output tile, and the buffers and per-lane offsets
+    // of its A rows, weight strips and scales.
+    struct item_ctx {
+        int nb, row0, rows;
+        __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc, s_rsrc;
+        int a_gather[GROUPED ? A_PW : 1];  // grouped: the gathered rows' offsets
+        int b_off[B_PW > 0 ? B_PW : 1];
+        int s_strip[NS];  // byte offset of strip j's scales in s_rsrc
+    };
     // SwiGLU (grouped): local strip s is gate strip (s even) or up strip (s odd) of slice
     // nb * BS / 2 + s / 2; otherwise strip strip0 + s.
-    const bool swiglu = GROUPED && a.swiglu_strips > 0;
-    auto wstrip = [&](int s_local) -> int {
+    auto wstrip = [&](int nb, int s_local) -> int {
         if (swiglu) {
             const int slice = nb * (BS / 2) + (s_local >> 1);
             return slice < a.swiglu_strips ? slice + ((s_local & 1) ? a.swiglu_strips : 0) : -1;
         }
-        return strip0 + s_local < a.strips ? strip0 + s_local : -1;
+        return nb * BS + s_local < a.strips ? nb * BS + s_local : -1;
     };
-    const int kt_begin = split * a.tiles_per_split;
-    const int kt_end = min(kt_begin + a.tiles_per_split, a.ktiles);
-    const uint8_t* wbase = a.w + (GROUPED ? expert * a.w_expert_bytes : 0);
-    const void* sbase = static_cast<const uint8_t*>(a.scale) + (GROUPED ? expert * a.s_expert_bytes : 0);
+    auto locate = [&](int item, item_ctx& c) -> bool {  // false: an idle grouped tile
+        int expert = 0;
+        if constexpr (GROUPED) {
+            const int tile = item / a.n_blocks;
+            c.nb = item % a.n_blocks;
+            expert = a.tiles[3 * tile];
+            c.row0 = a.tiles[3 * tile + 1];
+            c.rows = a.tiles[3 * tile + 2];
+            if (c.rows <= 0) return false;  // uniform across the workgroup
+        } else {
+            const int mb = item % a.m_blocks;
+            c.nb = item / a.m_blocks;
+            c.row0 = mb * BM;
+            c.rows = min(BM, a.m - c.row0);
+        }
+        const int strip0 = c.nb * BS;
+        // PERSIST: lane-derived offsets come from an opaque copy of the lane id, so that the
+        // compiler recomputes them per item instead of hoisting them out of the item loop and
+        // keeping them live across the K loop (the tall tile has no registers to spare).
+        int llane = lane;
+        if constexpr (PERSIST) asm volatile("" : "+v"(llane));
+        const int lrow_l = llane / SLOTS;
+        const uint8_t* wbase = a.w + (GROUPED ? expert * a.w_expert_bytes : 0);
+        const uint8_t* sbase = static_cast<const uint8_t*>(a.scale) + (GROUPED ? expert * a.s_expert_bytes : 0);
+        // A source: row-major rows of ARB bytes per K tile. Plain calls address rows from row0
+        // and bound the buffer at `rows` rows; grouped calls gather rows through row_index
+        // (the host checks every offset stays below kOOB) and keep the offsets in registers.
+        if constexpr (GROUPED) {
+            c.a_rsrc = make_rsrc(a.x, static_cast<uint32_t>(kOOB));
+#pragma unroll
+            for (int i = 0; i < A_PW; ++i) {
+                const int r = (wave * A_PW + i) * RPC + lrow_l;
+                int src = -1;
+                if (r < c.rows) src = a.row_index != nullptr ? a.row_index[c.row0 + r] : c.row0 + r;
+                c.a_gather[i] = src < 0 ? kOOB : src * a_stride;
+            }
+        } else {
+            const uint8_t* base = A8 ? a.xq : reinterpret_cast<const uint8_t*>(a.x);
+            c.a_rsrc = make_rsrc(base + static_cast<int64_t>(c.row0) * a_stride, static_cast<uint32_t>(c.rows * a_stride));
+        }
+        // Weights: this workgroup's strips are contiguous, ktiles * TB bytes each (with SwiGLU,
+        // two runs of them, addressed from the expert's first strip).
+        c.b_rsrc = swiglu ? make_rsrc(wbase, static_cast<uint32_t>(a.strips * strip_bytes))
+                          : make_rsrc(wbase + static_cast<int64_t>(strip0) * strip_bytes,
+                                      static_cast<uint32_t>(min(BS, a.strips - strip0) * strip_bytes));
+#pragma unroll
+        for (int i = 0; i < B_PW; ++i) {
+            const int ch = wave * B_PW + i;
+            const int sl = ch / (TB / 1024), in_strip = (ch % (TB / 1024)) * 1024 + llane * 16;
+            if (swiglu) {
+                const int ws = wstrip(c.nb, sl);
+                c.b_off[i] = ws >= 0 ? ws * strip_bytes + in_strip : kOOB;
+            } else {
+                c.b_off[i] = sl * strip_bytes + in_strip;
+            }
+        }
+        // Scales of this workgroup's strips ([strip][group][scale_cols], ES bytes each); strips
+        // past N read as zero.
+        c.s_rsrc = swiglu ? make_rsrc(sbase, static_cast<uint32_t>(a.strips * s_row))
+                          : make_rsrc(sbase + static_cast<int64_t>(strip0) * s_row,
+                                      static_cast<uint32_t>(min(BS, a.strips - strip0) * s_row));
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            if (swiglu) {
+                const int ws = wstrip(c.nb, wn * NS + j);
+                c.s_strip[j] = ws >= 0 ? ws * s_row : kOOB;
+            } else {
+                c.s_strip[j] = (wn * NS + j) * s_row;
+            }
+        }
+        return true;
+    };
 
-    // A source: row-major rows of ARB bytes per K tile. Plain calls address rows from row0 and
-    // bound the buffer at `rows` rows; grouped calls gather rows through row_index (the host
-    // checks every offset stays below kOOB).
-    const int a_stride = A8 ? a.ktiles * kTileK : a.k * 2;
-    __amdgpu_buffer_rsrc_t a_rsrc;
-    if constexpr (GROUPED) {
-        a_rsrc = make_rsrc(a.x, static_cast<uint32_t>(kOOB));
-    } else {
-        const uint8_t* base = A8 ? a.xq : reinterpret_cast<const uint8_t*>(a.x);
-        a_rsrc = make_rsrc(base + static_cast<int64_t>(row0) * a_stride, static_cast<uint32_t>(rows * a_stride));
-    }
     // Chunk c of the A tile is rows c*RPC .. c*RPC+RPC-1; lane L of its load writes slot L % SLOTS
     // of row c*RPC + L / SLOTS, which holds the row's 16-byte column (slot ^ row % SLOTS): the XOR
     // swizzle puts the 16 rows of one MFMA fragment read in 16 different bank groups.
-    // Plain calls recompute the offsets per load (rows past `rows` fall outside the buffer);
-    // grouped calls keep the gathered ones in registers.
-    const int lrow = lane / SLOTS, lslot = lane % SLOTS;
-    int a_gather[GROUPED ? A_PW : 1];
-    if constexpr (GROUPED) {
-#pragma unroll
-        for (int i = 0; i < A_PW; ++i) {
-            const int r = (wave * A_PW + i) * RPC + lrow;
-            int src = -1;
-            if (r < rows) src = a.row_index != nullptr ? a.row_index[row0 + r] : row0 + r;
-            a_gather[i] = src < 0 ? kOOB : src * a_stride;
-        }
-    }
-    auto a_offset = [&](int i, int kt) -> int {
+    // Plain calls recompute the offsets per load (rows past `rows` fall outside the buffer).
+    auto a_offset = [&](const item_ctx& c, int i, int kt) -> int {
         const int r = (wave * A_PW + i) * RPC + lrow;
-        const int c = lslot ^ (r % SLOTS);
-        const int row_off = GROUPED ? a_gather[GROUPED ? i : 0] : r * a_stride;
+        const int col = lslot ^ (r % SLOTS);
+        const int row_off = GROUPED ? c.a_gather[GROUPED ? i : 0] : r * a_stride;
         if constexpr (!UNIFORM) {
-            if (kt * kTileK + c * 8 >= a.k) return kOOB;  // K tail (bf16 x only)
+            if (kt * kTileK + col * 8 >= a.k) return kOOB;  // K tail (bf16 x only)
         }
-        return row_off + c * 16;
+        return row_off + col * 16;
     };
-    // Weights: this workgroup's strips are contiguous, ktiles * TB bytes each (with SwiGLU,
-    // two runs of them, addressed from the expert's first strip).
-    const int strip_bytes = a.ktiles * TB;
-    const __amdgpu_buffer_rsrc_t b_rsrc =
-        swiglu ? make_rsrc(wbase, static_cast<uint32_t>(a.strips * strip_bytes))
-               : make_rsrc(wbase + static_cast<int64_t>(strip0) * strip_bytes,
-                           static_cast<uint32_t>(min(BS, a.strips - strip0) * strip_bytes));
-    int b_off[B_PW > 0 ? B_PW : 1];
-#pragma unroll
-    for (int i = 0; i < B_PW; ++i) {
-        const int c = wave * B_PW + i;
-        const int sl = c / (TB / 1024), in_strip = (c % (TB / 1024)) * 1024 + lane * 16;
-        if (swiglu) {
-            const int ws = wstrip(sl);
-            b_off[i] = ws >= 0 ? ws * strip_bytes + in_strip : kOOB;
-        } else {
-            b_off[i] = sl * strip_bytes + in_strip;
-        }
-    }
-
-    auto load_breg = [&](u32x4_t (&dst)[NS][TB / 1024], int kt) {
+    auto load_breg = [&](const item_ctx& c, u32x4_t (&dst)[NS][TB / 1024], int kt) {
 #pragma unroll
         for (int j = 0; j < NS; ++j)
 #pragma unroll
             for (int h = 0; h < TB / 1024; ++h)
-                dst[j][h] = buffer_load16(b_rsrc, (wn * NS + j) * strip_bytes + h * 1024 + lane * 16, kt * TB);
+                dst[j][h] = buffer_load16(c.b_rsrc, (wn * NS + j) * strip_bytes + h * 1024 + lane * 16, kt * TB);
     };
-    auto issue = [&](int kt, int stage) {
+    auto issue = [&](const item_ctx& c, int kt, int stage) {
         uint8_t* sa = lds + stage * STAGE;
 #pragma unroll
         for (int i = 0; i < A_PW; ++i)
             if (A_CHUNKS % NW == 0 || wave * A_PW + i < A_CHUNKS)  // wave-uniform
-                buffer_load_lds16(a_rsrc, sa + (wave * A_PW + i) * 1024, a_offset(i, kt), kt * ARB);
+                buffer_load_lds16(c.a_rsrc, sa + (wave * A_PW + i) * 1024, a_offset(c, i, kt), kt * ARB);
 #pragma unroll
         for (int i = 0; i < B_PW; ++i)
             if (B_CHUNKS % NW == 0 || wave * B_PW + i < B_CHUNKS)  // wave-uniform
-                buffer_load_lds16(b_rsrc, sa + A_STAGE + (wave * B_PW + i) * 1024, b_off[i], kt * TB);
+                buffer_load_lds16(c.b_rsrc, sa + A_STAGE + (wave * B_PW + i) * 1024, c.b_off[i], kt * TB);
     };
-
-    // Scales of this workgroup's strips ([strip][group][scale_cols], ES bytes each), loaded as
-    // raw bits one K step ahead and converted when used, so that no wait on them stalls the
-    // tile loads in flight. Strips past N read as zero.
-    const bool bf16_scale = a.scale_dtype == PLM_BF16;
-    const int s_row = a.groups * a.scale_cols * ES;  // bytes per strip
-    const __amdgpu_buffer_rsrc_t s_rsrc =
-        swiglu ? make_rsrc(sbase, static_cast<uint32_t>(a.strips * s_row))
-               : make_rsrc(static_cast<const uint8_t*>(sbase) + static_cast<int64_t>(strip0) * s_row,
-                           static_cast<uint32_t>(min(BS, a.strips - strip0) * s_row));
-    const int s_lane = a.scale_cols == 1 ? 0 : col16 * ES;
-    int s_strip[NS];  // byte offset of strip j's scales in s_rsrc
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-        if (swiglu) {
-            const int ws = wstrip(wn * NS + j);
-            s_strip[j] = ws >= 0 ? ws * s_row : kOOB;
-        } else {
-            s_strip[j] = (wn * NS + j) * s_row;
-        }
-    }
-    auto scale_bits = [&](int j, int kt, int t) -> uint32_t {
-        int voff = s_lane + s_strip[j], soff = 0;
+    // Scales are loaded as raw bits one K step ahead and converted when used, so that no wait
+    // on them stalls the tile loads in flight.
+    auto scale_bits = [&](const item_ctx& c, int j, int kt, int t) -> uint32_t {
+        int voff = s_lane + c.s_strip[j], soff = 0;
         if constexpr (UNIFORM) soff = uniform(kt * kTileK / a.group_size) * a.scale_cols * ES;
         else voff += (kt * kTileK + 32 * t + 8 * kq) / a.group_size * a.scale_cols * ES;
-        if constexpr (WIDE) return buffer_load_u32(s_rsrc, voff, soff);
-        else return buffer_load_u16(s_rsrc, voff, soff);
+        if constexpr (WIDE) return buffer_load_u32(c.s_rsrc, voff, soff);
+        else return buffer_load_u16(c.s_rsrc, voff, soff);
     };
 
-    f32x4_t acc[MT][NS];
+    // Epilogue: lane holds column col16 of strip (strip0 + wn*NS + j), rows 4*kq + r of m tile i.
+    auto epilogue = [&](const item_ctx& c, f32x4_t (&acc)[MT][NS], int last_stage) {
+        const int strip0 = c.nb * BS;
+        int ekq = kq, ecol = col16, elane = lane;
+        if constexpr (PERSIST) asm volatile("" : "+v"(ekq), "+v"(ecol), "+v"(elane));
+        if constexpr (GROUPED && NS % 2 == 0) {
+            if (swiglu) {  // gate strip j, up strip j + 1 of slice nb * BS / 2 + (wn * NS + j) / 2
+                const int inter = a.swiglu_strips * kTileN;
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+                for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int j = 0; j < NS; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    uint32_t sc[NS][ST];
-    u32x4_t wreg[NS][TB / 1024], wnext[NS][TB / 1024];  // BREG: this and the next step's tiles
-    if (kt_begin < kt_end) {
+                    for (int j = 0; j < NS; j += 2) {
+                        const int col = (c.nb * (BS / 2) + (wn * NS + j) / 2) * kTileN + ecol;
 #pragma unroll
-        for (int j = 0; j < NS; ++j)
-#pragma unroll
-            for (int t = 0; t < ST; ++t) sc[j][t] = scale_bits(j, kt_begin, t);
-        issue(kt_begin, 0);
-        if constexpr (BREG) load_breg(wreg, kt_begin);
-    }
-
-    for (int kt = kt_begin; kt < kt_end; ++kt) {
-        const int stage = (kt - kt_begin) & 1;
-        // This step's tiles have landed (they are the only loads in flight) and every
-        // wavefront is done with the other stage, which the next loads overwrite.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        uint32_t scn[NS][ST];
-        const bool more = kt + 1 < kt_end;
-        if (more) {
-#pragma unroll
-            for (int j = 0; j < NS; ++j)
-#pragma unroll
-                for (int t = 0; t < ST; ++t) scn[j][t] = scale_bits(j, kt + 1, t);
-            issue(kt + 1, stage ^ 1);
-            if constexpr (BREG) load_breg(wnext, kt + 1);
+                        for (int r = 0; r < 4; ++r) {
+                            const int lr = wm * MT * 16 + i * 16 + 4 * ekq + r;
+                            if (lr < c.rows && col < inter)
+                                a.y[static_cast<int64_t>(c.row0 + lr) * inter + col] = static_cast<uint16_t>(
+                                    to_bits16<BF16>(silu_times<BF16>(round_to<BF16>(acc[i][j][r]),
+                                                                     round_to<BF16>(acc[i][j + 1][r]))));
+                        }
+                    }
+                return;
+            }
         }
-
-        const uint8_t* sa = lds + stage * STAGE;
-        const uint8_t* sb = sa + A_STAGE;
-        u32x4_t wv[NS][TB / 1024];
-#pragma unroll
-        for (int j = 0; j < NS; ++j)
-#pragma unroll
-            for (int h = 0; h < TB / 1024; ++h)
-                wv[j][h] = BREG ? wreg[j][h]
-                                : *reinterpret_cast<const u32x4_t*>(sb + (wn * NS + j) * TB + h * 1024 + lane * 16);
-
-        if constexpr (A8) {
+        // With 16-byte aligned output rows, each m tile goes through the wavefront's own LDS area
+        // (16 rows of 16 * NS columns; the row pitch is padded by 16 bytes so the four row groups
+        // of one write land in different banks) and leaves as one 16-byte store per 8 columns of
+        // a row, instead of a 2-byte store per element. Separate instantiations (VO) for the
+        // launches that take it: compiled into the split-K kernels too, it changed their register
+        // allocation and made down at M = 1024 10 % slower. PERSIST stages in the stage the last
+        // K step read (the other one holds the next item's first loads).
+        if (VO && a.splits == 1 && (a.n & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
+            constexpr int EROW = 32 * NS + 16;
+            static_assert(1024 + NW * 16 * EROW <= (PERSIST ? STAGE : 2 * STAGE), "epilogue staging fits");
+            __syncthreads();  // every wavefront is past the K loop's last reads of the stages
+            // Past the split-K arrival flag.
+            uint8_t* ew = lds + (PERSIST ? last_stage * STAGE : 0) + 1024 + wave * 16 * EROW;
+            const int col0 = (strip0 + wn * NS) * kTileN;
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
-                const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
-                const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(ra + (((2 * kq) ^ (col16 & 7)) * 16));
-                const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(ra + (((2 * kq + 1) ^ (col16 & 7)) * 16));
-                const i32x8_t av = __builtin_bit_cast(i32x8_t, u32x8_cat(a0, a1));
-#pragma unroll
-                for (int j = 0; j < NS; ++j) {
-                    const i32x8_t bv = __builtin_bit_cast(i32x8_t, u32x8_cat(wv[j][0], wv[j][TB / 1024 - 1]));
-                    const f32x4_t part = mfma16x16x128_fp8(av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(scale_from_bits<WIDE>(sc[j][0], bf16_scale), part[r], acc[i][j][r]);
-                }
-            }
-        } else if constexpr (PIPE_A) {
-            // The MT x fragments of a K slice are held in registers and each is re-read for
-            // the next slice right after its MFMAs, so a fragment read has a whole slice of
-            // MFMAs (MT * NS) to land instead of the next two.
-            auto frag = [&](int i, int t) {
-                const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
-                return *reinterpret_cast<const u32x4_t*>(ra + (((4 * t + kq) ^ col16) * 16));
-            };
-            u32x4_t af[PD];
-#pragma unroll
-            for (int i = 0; i < PD; ++i) af[i] = frag(i, 0);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                u32x4_t b[NS];
-#pragma unroll
-                for (int j = 0; j < NS; ++j) {
-                    const float raw = scale_from_bits<WIDE>(sc[j][UNIFORM ? 0 : t], bf16_scale);
-                    if constexpr (F == PLM_INT4) {
-                        b[j] = dq_int4<BF16>(wv[j][0][t], make_int4_scale<BF16>(raw));
-                    } else {
-                        b[j] = dq_fp8<BF16>(wv[j][t >> 1][(t & 1) * 2], wv[j][t >> 1][(t & 1) * 2 + 1],
-                                            round_to<BF16>(raw));
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < PD; ++i) {
-#pragma unroll
-                    for (int j = 0; j < NS; ++j) acc[i][j] = mfma16x16x32<BF16>(af[i], b[j], acc[i][j]);
-                    if (t < 3) af[i] = frag(i, t + 1);
-                    __builtin_amdgcn_sched_barrier(0);  // keep the read here, a slice ahead
-                }
-#pragma unroll
-                for (int i = PD; i < MT; ++i) {
-                    const u32x4_t a1 = frag(i, t);
-#pragma unroll
-                    for (int j = 0; j < NS; ++j) acc[i][j] = mfma16x16x32<BF16>(a1, b[j], acc[i][j]);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                // Dequantize this 32-wide K slice of every strip once, then stream the x
-                // fragments past it: each weight fragment feeds MT MFMAs.
-                u32x4_t b[NS];
-#pragma unroll
-                for (int j = 0; j < NS; ++j) {
-                    const float raw = scale_from_bits<WIDE>(sc[j][UNIFORM ? 0 : t], bf16_scale);
-                    if constexpr (F == PLM_INT4) {
-                        b[j] = dq_int4<BF16>(wv[j][0][t], make_int4_scale<BF16>(raw));
-                    } else {
-                        b[j] = dq_fp8<BF16>(wv[j][t >> 1][(t & 1) * 2], wv[j][t >> 1][(t & 1) * 2 + 1],
-                                            round_to<BF16>(raw));
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < MT; ++i) {
-                    const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
-                    const u32x4_t af = *reinterpret_cast<const u32x4_t*>(ra + (((4 * t + kq) ^ col16) * 16));
-#pragma unroll
-                    for (int j = 0; j < NS; ++j) acc[i][j] = mfma16x16x32<BF16>(af, b[j], acc[i][j]);
-                }
-            }
-        }
-        if (more) {
-#pragma unroll
-            for (int j = 0; j < NS; ++j)
-#pragma unroll
-                for (int t = 0; t < ST; ++t) sc[j][t] = scn[j][t];
-            if constexpr (BREG) {
 #pragma unroll
                 for (int j = 0; j < NS; ++j)
 #pragma unroll
-                    for (int h = 0; h < TB / 1024; ++h) wreg[j][h] = wnext[j][h];
+                    for (int r = 0; r < 4; ++r)
+                        *reinterpret_cast<uint16_t*>(ew + (4 * ekq + r) * EROW + (16 * j + ecol) * 2) =
+                            static_cast<uint16_t>(to_bits16<BF16>(acc[i][j][r]));
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int c0 = 0; c0 < 32 * NS; c0 += 64) {  // 16 rows x 2 * NS chunks of 8 columns
+                    const int ch16 = c0 + elane;
+                    if (ch16 < 32 * NS) {
+                        const int row = ch16 / (2 * NS), ch = ch16 % (2 * NS);
+                        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ew + row * EROW + ch * 16);
+                        const int lr = wm * MT * 16 + i * 16 + row;
+                        const int col = col0 + ch * 8;
+                        if (lr < c.rows && col < a.n)
+                            *reinterpret_cast<u32x4_t*>(a.y + static_cast<int64_t>(c.row0 + lr) * a.n + col) = v;
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
             }
+            return;
         }
-    }
-
-    if constexpr (A8) {
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = row0 + wm * MT * 16 + i * 16 + 4 * kq + r;
-                const float sx = a.x_scale[min(row, a.m - 1)];
+            for (int j = 0; j < NS; ++j) {
+                const int col = (strip0 + wn * NS + j) * kTileN + ecol;
 #pragma unroll
-                for (int j = 0; j < NS; ++j) acc[i][j][r] *= sx;
+                for (int r = 0; r < 4; ++r) {
+                    const int lr = wm * MT * 16 + i * 16 + 4 * ekq + r;
+                    if (lr < c.rows && col < a.n)
+                        a.y[static_cast<int64_t>(c.row0 + lr) * a.n + col] =
+                            static_cast<uint16_t>(to_bits16<BF16>(acc[i][j][r]));
+                }
             }
-    }
+    };
 
-    // Split K: every workgroup stores its accumulators in lane order (16 bytes per lane per
-    // MFMA tile, so each store instruction is one contiguous 1 KiB) into its own slot of the
-    // work tile's partial area; the last workgroup to arrive reloads all slots and sums them
-    // in split order, so the result does not depend on arrival order.
-    // PLM_MEASURE_SKIP_REDUCTION (a measurement build only, never the shipped library): the
-    // split workgroups write their own partial sums as the result, so timing the same launches
-    // with and without it gives the cost of the split-K reduction (wrong results).
+    int pos = 0;
+    int item = item_at(0);
+    if (item < 0) return;
+    item_ctx cur;
+    while (!locate(item, cur)) {
+        if (!PERSIST) return;
+        item = item_at(++pos);
+        if (item < 0) return;
+    }
+    int stage0 = 0;      // the stage of this item's first K step
+    bool loaded = false;  // its first K step is already in flight (PERSIST)
+    for (;;) {
+        f32x4_t acc[MT][NS];
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < NS; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+        uint32_t sc[NS][ST];
+        u32x4_t wreg[NS][TB / 1024], wnext[NS][TB / 1024];  // BREG: this and the next step's tiles
+        if (kt_begin < kt_end) {
+#pragma unroll
+            for (int j = 0; j < NS; ++j)
+#pragma unroll
+                for (int t = 0; t < ST; ++t) sc[j][t] = scale_bits(cur, j, kt_begin, t);
+            if (!loaded) issue(cur, kt_begin, stage0);
+            if constexpr (BREG) load_breg(cur, wreg, kt_begin);
+        }
+
+        for (int kt = kt_begin; kt < kt_end; ++kt) {
+            const int stage = stage0 ^ ((kt - kt_begin) & 1);
+            // This step's tiles have landed (they are the only loads in flight) and every
+            // wavefront is done with the other stage, which the next loads overwrite.
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            uint32_t scn[NS][ST];
+            const bool more = kt + 1 < kt_end;
+            if (more) {
+#pragma unroll
+                for (int j = 0; j < NS; ++j)
+#pragma unroll
+                    for (int t = 0; t < ST; ++t) scn[j][t] = scale_bits(cur, j, kt + 1, t);
+                issue(cur, kt + 1, stage ^ 1);
+                if constexpr (BREG) load_breg(cur, wnext, kt + 1);
+            }
+
+            const uint8_t* sa = lds + stage * STAGE;
+            const uint8_t* sb = sa + A_STAGE;
+            u32x4_t wv[NS][TB / 1024];
+#pragma unroll
+            for (int j = 0; j < NS; ++j)
+#pragma unroll
+                for (int h = 0; h < TB / 1024; ++h)
+                    wv[j][h] = BREG ? wreg[j][h]
+                                    : *reinterpret_cast<const u32x4_t*>(sb + (wn * NS + j) * TB + h * 1024 + lane * 16);
+
+            if constexpr (A8) {
+#pragma unroll
+                for (int i = 0; i < MT; ++i) {
+                    const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
+                    const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(ra + (((2 * kq) ^ (col16 & 7)) * 16));
+                    const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(ra + (((2 * kq + 1) ^ (col16 & 7)) * 16));
+                    const i32x8_t av = __builtin_bit_cast(i32x8_t, u32x8_cat(a0, a1));
+#pragma unroll
+                    for (int j = 0; j < NS; ++j) {
+                        const i32x8_t bv = __builtin_bit_cast(i32x8_t, u32x8_cat(wv[j][0], wv[j][TB / 1024 - 1]));
+                        const f32x4_t part = mfma16x16x128_fp8(av, bv, f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(scale_from_bits<WIDE>(sc[j][0], bf16_scale), part[r], acc[i][j][r]);
+                    }
+                }
+            } else if constexpr (PIPE_A) {
+                // The MT x fragments of a K slice are held in registers and each is re-read for
+                // the next slice right after its MFMAs, so a fragment read has a whole slice of
+                // MFMAs (MT * NS) to land instead of the next two.
+                auto frag = [&](int i, int t) {
+                    const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
+                    return *reinterpret_cast<const u32x4_t*>(ra + (((4 * t + kq) ^ col16) * 16));
+                };
+                u32x4_t af[PD];
+#pragma unroll
+                for (int i = 0; i < PD; ++i) af[i] = frag(i, 0);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    u32x4_t b[NS];
+#pragma unroll
+                    for (int j = 0; j < NS; ++j) {
+                        const float raw = scale_from_bits<WIDE>(sc[j][UNIFORM ? 0 : t], bf16_scale);
+                        if constexpr (F == PLM_INT4) {
+                            b[j] = dq_int4<BF16>(wv[j][0][t], make_int4_scale<BF16>(raw));
+                        } else {
+                            b[j] = dq_fp8<BF16>(wv[j][t >> 1][(t & 1) * 2], wv[j][t >> 1][(t & 1) * 2 + 1],
+                                                round_to<BF16>(raw));
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < PD; ++i) {
+#pragma unroll
+                        for (int j = 0; j < NS; ++j) acc[i][j] = mfma16x16x32<BF16>(af[i], b[j], acc[i][j]);
+                        if (t < 3) af[i] = frag(i, t + 1);
+                        __builtin_amdgcn_sched_barrier(0);  // keep the read here, a slice ahead
+                    }
+#pragma unroll
+                    for (int i = PD; i < MT; ++i) {
+                        const u32x4_t a1 = frag(i, t);
+#pragma unroll
+                        for (int j = 0; j < NS; ++j) acc[i][j] = mfma16x16x32<BF16>(a1, b[j], acc[i][j]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    // Dequantize this 32-wide K slice of every strip once, then stream the x
+                    // fragments past it: each weight fragment feeds MT MFMAs.
+                    u32x4_t b[NS];
+#pragma unroll
+                    for (int j = 0; j < NS; ++j) {
+                        const float raw = scale_from_bits<WIDE>(sc[j][UNIFORM ? 0 : t], bf16_scale);
+                        if constexpr (F == PLM_INT4) {
+                            b[j] = dq_int4<BF16>(wv[j][0][t], make_int4_scale<BF16>(raw));
+                        } else {
+                            b[j] = dq_fp8<BF16>(wv[j][t >> 1][(t & 1) * 2], wv[j][t >> 1][(t & 1) * 2 + 1],
+                                                round_to<BF16>(raw));
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < MT; ++i) {
+                        const uint8_t* ra = sa + (wm * MT * 16 + i * 16 + col16) * ARB;
+                        const u32x4_t af = *reinterpret_cast<const u32x4_t*>(ra + (((4 * t + kq) ^ col16) * 16));
+#pragma unroll
+                        for (int j = 0; j < NS; ++j) acc[i][j] = mfma16x16x32<BF16>(af, b[j], acc[i][j]);
+                    }
+                }
+            }
+            if (more) {
+#pragma unroll
+                for (int j = 0; j < NS; ++j)
+#pragma unroll
+                    for (int t = 0; t < ST; ++t) sc[j][t] = scn[j][t];
+                if constexpr (BREG) {
+#pragma unroll
+                    for (int j = 0; j < NS; ++j)
+#pragma unroll
+                        for (int h = 0; h < TB / 1024; ++h) wreg[j][h] = wnext[j][h];
+                }
+            }
+        }
+        // The stage the last K step read; the other one is free.
+        const int last_stage = stage0 ^ ((kt_end - 1 - kt_begin) & 1);
+
+        // PERSIST: the next item's first K step goes into the free stage now, so that its loads
+        // are in flight during this item's epilogue (which stages through last_stage only).
+        int next = -1;
+        item_ctx nxt;
+        if constexpr (PERSIST) {
+            for (;;) {
+                next = item_at(++pos);
+                if (next < 0 || locate(next, nxt)) break;
+            }
+            if (next >= 0) issue(nxt, kt_begin, last_stage ^ 1);
+        }
+
+        if constexpr (A8) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = cur.row0 + wm * MT * 16 + i * 16 + 4 * kq + r;
+                    const float sx = a.x_scale[min(row, a.m - 1)];
+#pragma unroll
+                    for (int j = 0; j < NS; ++j) acc[i][j][r] *= sx;
+                }
+        }
+
+        // Split K (never PERSIST): every workgroup stores its accumulators in lane order (16
+        // bytes per lane per MFMA tile, so each store instruction is one contiguous 1 KiB) into
+        // its own slot of the work tile's partial area; the last workgroup to arrive reloads all
+        // slots and sums them in split order, so the result does not depend on arrival order.
+        // PLM_MEASURE_SKIP_REDUCTION (a measurement build only, never the shipped library): the
+        // split workgroups write their own partial sums as the result, so timing the same
+        // launches with and without it gives the cost of the split-K reduction (wrong results).
 #ifndef PLM_MEASURE_SKIP_REDUCTION
 #define PLM_MEASURE_SKIP_REDUCTION 0
 #endif
-    if (a.splits > 1 && !PLM_MEASURE_SKIP_REDUCTION) {
-        constexpr int TILE_BYTES = MT * NS * NT * 16;
-        const __amdgpu_buffer_rsrc_t p_rsrc = make_rsrc(
-            reinterpret_cast<uint8_t*>(a.partial) + static_cast<int64_t>(blockIdx.x) * a.splits * TILE_BYTES,
-            static_cast<uint32_t>(a.splits * TILE_BYTES));
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-#pragma unroll
-            for (int j = 0; j < NS; ++j)
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[i][j]), p_rsrc,
-                                                       ((i * NS + j) * NT + tid) * 16, split * TILE_BYTES, kCoherent);
-        if (!arrive_last(&a.counters[blockIdx.x], static_cast<uint32_t>(a.splits), &last_flag)) return;
-        for (int sp = 0; sp < a.splits; ++sp) {
+        if (!PERSIST && a.splits > 1 && !PLM_MEASURE_SKIP_REDUCTION) {
+            constexpr int TILE_BYTES = MT * NS * NT * 16;
+            const __amdgpu_buffer_rsrc_t p_rsrc = make_rsrc(
+                reinterpret_cast<uint8_t*>(a.partial) + static_cast<int64_t>(blockIdx.x) * a.splits * TILE_BYTES,
+                static_cast<uint32_t>(a.splits * TILE_BYTES));
 #pragma unroll
             for (int i = 0; i < MT; ++i)
 #pragma unroll
-                for (int j = 0; j < NS; ++j) {
-                    const f32x4_t v = __builtin_bit_cast(
-                        f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(p_rsrc, ((i * NS + j) * NT + tid) * 16,
-                                                                       sp * TILE_BYTES, kCoherent));
-                    acc[i][j] = sp == 0 ? v : acc[i][j] + v;
-                }
-        }
-    }
-
-    if constexpr (GROUPED && NS % 2 == 0) {
-        if (swiglu) {  // gate strip j, up strip j + 1 of slice nb * BS / 2 + (wn * NS + j) / 2
-            const int inter = a.swiglu_strips * kTileN;
+                for (int j = 0; j < NS; ++j)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[i][j]), p_rsrc,
+                                                           ((i * NS + j) * NT + tid) * 16, split * TILE_BYTES, kCoherent);
+            if (!arrive_last(&a.counters[blockIdx.x], static_cast<uint32_t>(a.splits), &last_flag)) return;
+            for (int sp = 0; sp < a.splits; ++sp) {
 #pragma unroll
-            for (int i = 0; i < MT; ++i)
+                for (int i = 0; i < MT; ++i)
 #pragma unroll
-                for (int j = 0; j < NS; j += 2) {
-                    const int col = (nb * (BS / 2) + (wn * NS + j) / 2) * kTileN + col16;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int lr = wm * MT * 16 + i * 16 + 4 * kq + r;
-                        if (lr < rows && col < inter)
-                            a.y[static_cast<int64_t>(row0 + lr) * inter + col] = static_cast<uint16_t>(
-                                to_bits16<BF16>(silu_times<BF16>(round_to<BF16>(acc[i][j][r]),
-                                                                 round_to<BF16>(acc[i][j + 1][r]))));
+                    for (int j = 0; j < NS; ++j) {
+                        const f32x4_t v = __builtin_bit_cast(
+                            f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(p_rsrc, ((i * NS + j) * NT + tid) * 16,
+                                                                           sp * TILE_BYTES, kCoherent));
+                        acc[i][j] = sp == 0 ? v : acc[i][j] + v;
                     }
-                }
-            return;
-        }
-    }
-    // Epilogue: lane holds column col16 of strip (strip0 + wn*NS + j), rows 4*kq + r of m tile i.
-    // With 16-byte aligned output rows, each m tile goes through the wavefront's own LDS area
-    // (16 rows of 16 * NS columns; the row pitch is padded by 16 bytes so the four row groups
-    // of one write land in different banks) and leaves as one 16-byte store per 8 columns of a
-    // row, instead of a 2-byte store per element. Separate instantiations (VO) for the launches
-    // that take it: compiled into the split-K kernels too, it changed their register
-    // allocation and made down at M = 1024 10 % slower.
-    if (VO && a.splits == 1 && (a.n & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
-        constexpr int EROW = 32 * NS + 16;
-        static_assert(1024 + NW * 16 * EROW <= 2 * STAGE, "epilogue staging fits the stages");
-        __syncthreads();  // every wavefront is past the K loop's last reads of the stages
-        uint8_t* ew = lds + 1024 + wave * 16 * EROW;  // past the split-K arrival flag
-        const int col0 = (strip0 + wn * NS) * kTileN;
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-#pragma unroll
-            for (int j = 0; j < NS; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    *reinterpret_cast<uint16_t*>(ew + (4 * kq + r) * EROW + (16 * j + col16) * 2) =
-                        static_cast<uint16_t>(to_bits16<BF16>(acc[i][j][r]));
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int c0 = 0; c0 < 32 * NS; c0 += 64) {  // 16 rows x 2 * NS chunks of 8 columns
-                const int c = c0 + lane;
-                if (c < 32 * NS) {
-                    const int row = c / (2 * NS), ch = c % (2 * NS);
-                    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ew + row * EROW + ch * 16);
-                    const int lr = wm * MT * 16 + i * 16 + row;
-                    const int col = col0 + ch * 8;
-                    if (lr < rows && col < a.n)
-                        *reinterpret_cast<u32x4_t*>(a.y + static_cast<int64_t>(row0 + lr) * a.n + col) = v;
-                }
-            }
-            __builtin_amdgcn_wave_barrier();
-        }
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < NS; ++j) {
-            const int col = (strip0 + wn * NS + j) * kTileN + col16;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int lr = wm * MT * 16 + i * 16 + 4 * kq + r;
-                if (lr < rows && col < a.n)
-                    a.y[static_cast<int64_t>(row0 + lr) * a.n + col] =
-                        static_cast<uint16_t>(to_bits16<BF16>(acc[i][j][r]));
             }
         }
+
+        epilogue(cur, acc, last_stage);
+        if (!PERSIST || next < 0) return;
+        cur = nxt;
+        stage0 = last_stage ^ 1;
+        loaded = true;
+    }
 }
 
 // Tile shapes: {WM, WN, MT, NS}.
@@ -847,26 +910,45 @@ int launch_mfma(const char* op, plm_format f, const void* x, bool bf16, const vo
 // rows are in the grouped (sorted) order and `row_index` optionally gathers them from x.
 // shape indexes kGroupedShapes (int4 experts only); 6 (256 x 256 tall) is for full blocks of rows.
 namespace {
-template <bool BF16, bool UNIFORM, bool WIDE>
-void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, hipStream_t s) {
-#define PLM_GROUPED_CASE(i)                                                                                   \
-    case i:                                                                                                   \
-        mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kGroupedShapes[i].wm, kGroupedShapes[i].wn,         \
-                    kGroupedShapes[i].mt, kGroupedShapes[i].ns, true>                                         \
-            <<<grid, kGroupedShapes[i].wm * kGroupedShapes[i].wn * 64, 0, s>>>(a);                            \
-        break;
-    switch (shape) {
-        PLM_GROUPED_CASE(0)
-        PLM_GROUPED_CASE(1)
-        PLM_GROUPED_CASE(2)
-        PLM_GROUPED_CASE(3)
-        PLM_GROUPED_CASE(5)
-        PLM_GROUPED_CASE(6)
-        default:
-            mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, kHuge.wm, kHuge.wn, kHuge.mt, kHuge.ns, true>
-                <<<grid, kHuge.wm * kHuge.wn * 64, 0, s>>>(a);
+// PERSIST launches: about one workgroup per slot the kernel can hold resident (occupancy per CU
+// times the CUs), a multiple of 8 so that every XCD gets the same number of workgroups, and
+// never more than the items.
+template <typename K>
+unsigned persistent_grid(K kernel, int threads, unsigned items) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const unsigned slots = static_cast<unsigned>(per_cu * cu_count()) & ~7u;
+    return std::max(8u, std::min(items, slots));
+}
+
+template <bool BF16, bool UNIFORM, bool WIDE, int I>
+void launch_grouped_one(const mfma_args& a, dim3 grid, bool persist, hipStream_t s) {
+    constexpr shape sh = kGroupedShapes[I];
+    constexpr int threads = sh.wm * sh.wn * 64;
+    if constexpr (I != 4) {  // the 256 x 256 two-row grid (unused by the MoE block) is never persistent
+        if (persist) {
+            auto* kernel = mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, sh.wm, sh.wn, sh.mt, sh.ns, true, true>;
+            grid.x = persistent_grid(kernel, threads, grid.x);
+            kernel<<<grid, threads, 0, s>>>(a);
+            return;
+        }
     }
-#undef PLM_GROUPED_CASE
+    mfma_kernel<PLM_INT4, BF16, UNIFORM, WIDE, false, true, sh.wm, sh.wn, sh.mt, sh.ns, true>
+        <<<grid, threads, 0, s>>>(a);
+}
+
+template <bool BF16, bool UNIFORM, bool WIDE>
+void launch_grouped_shape(const mfma_args& a, int shape, dim3 grid, bool persist, hipStream_t s) {
+    switch (shape) {
+        case 0: launch_grouped_one<BF16, UNIFORM, WIDE, 0>(a, grid, persist, s); break;
+        case 1: launch_grouped_one<BF16, UNIFORM, WIDE, 1>(a, grid, persist, s); break;
+        case 2: launch_grouped_one<BF16, UNIFORM, WIDE, 2>(a, grid, persist, s); break;
+        case 3: launch_grouped_one<BF16, UNIFORM, WIDE, 3>(a, grid, persist, s); break;
+        case 5: launch_grouped_one<BF16, UNIFORM, WIDE, 5>(a, grid, persist, s); break;
+        case 6: launch_grouped_one<BF16, UNIFORM, WIDE, 6>(a, grid, persist, s); break;
+        default: launch_grouped_one<BF16, UNIFORM, WIDE, 4>(a, grid, persist, s); break;
+    }
 }
 }  // namespace
 
@@ -917,18 +999,19 @@ int launch_grouped(const char* op, plm_format f, const void* x, bool bf16, const
     a.w_expert_bytes = ceil_div(n, kTileN) * ceil_div(k, kTileK) * tile_bytes(f);
     a.s_expert_bytes = static_cast<int64_t>(a.strips) * a.groups * a.scale_cols * dtype_size(scale_dtype);
     dim3 grid(static_cast<unsigned>(round_up(max_tiles * a.n_blocks, 8)), 1);  // whole XCD rounds
+    const bool persist = knobs().moe_persist;  // A/B measurements: measured slower
     const bool uniform = group_size % kTileK == 0;
     const bool wide = scale_dtype == PLM_FP32;
     const int mode = (bf16 ? 4 : 0) + (uniform ? 2 : 0) + (wide ? 1 : 0);
     switch (mode) {
-        case 0: launch_grouped_shape<false, false, false>(a, shape, grid, s); break;
-        case 1: launch_grouped_shape<false, false, true>(a, shape, grid, s); break;
-        case 2: launch_grouped_shape<false, true, false>(a, shape, grid, s); break;
-        case 3: launch_grouped_shape<false, true, true>(a, shape, grid, s); break;
-        case 4: launch_grouped_shape<true, false, false>(a, shape, grid, s); break;
-        case 5: launch_grouped_shape<true, false, true>(a, shape, grid, s); break;
-        case 6: launch_grouped_shape<true, true, false>(a, shape, grid, s); break;
-        default: launch_grouped_shape<true, true, true>(a, shape, grid, s); break;
+        case 0: launch_grouped_shape<false, false, false>(a, shape, grid, persist, s); break;
+        case 1: launch_grouped_shape<false, false, true>(a, shape, grid, persist, s); break;
+        case 2: launch_grouped_shape<false, true, false>(a, shape, grid, persist, s); break;
+        case 3: launch_grouped_shape<false, true, true>(a, shape, grid, persist, s); break;
+        case 4: launch_grouped_shape<true, false, false>(a, shape, grid, persist, s); break;
+        case 5: launch_grouped_shape<true, false, true>(a, shape, grid, persist, s); break;
+        case 6: launch_grouped_shape<true, true, false>(a, shape, grid, persist, s); break;
+        default: launch_grouped_shape<true, true, true>(a, shape, grid, persist, s); break;
     }
     PLM_HIP_LAUNCH_CHECK(op);
     return PLM_OK;

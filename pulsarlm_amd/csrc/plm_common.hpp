@@ -407,6 +407,7 @@ struct tuning {
     int moe_rows = 0;                  // PLM_MOE_ROWS=16/32/64
     bool moe_small_sort_off = false;   // PLM_MOE_SMALL_SORT=0
     bool moe_unfused = false;          // PLM_MOE_UNFUSED
+    bool moe_persist = false;          // PLM_MOE_PERSIST=1: persistent grouped launches
 };
 const tuning& knobs();
 

@@ -71,6 +71,7 @@ tuning parse_tuning() {
     if (const char* e = env("PLM_MOE_ROWS")) t.moe_rows = atoi(e);
     if (const char* e = env("PLM_MOE_SMALL_SORT")) t.moe_small_sort_off = e[0] == '0';
     t.moe_unfused = env("PLM_MOE_UNFUSED") != nullptr;
+    if (const char* e = env("PLM_MOE_PERSIST")) t.moe_persist = e[0] == '1';
     return t;
 }
 std::mutex g_tuning_mutex;

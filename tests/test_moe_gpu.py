@@ -281,3 +281,28 @@ def test_empty_inputs_every_entry_point():
     weights, chosen = ops.route_top_k_cuda(torch.empty((0, e), device="cuda"), 2)
     assert weights.shape == (0, 2) and chosen.shape == (0, 2)
     assert ops.silu_mul_cuda(torch.empty((0, 2 * inter), dtype=torch.bfloat16, device="cuda")).shape == (0, inter)
+
+
+@pytest.mark.parametrize("t,e,hidden,inter,top_k", [(256, 128, 2048, 768, 8), (4096, 128, 2048, 768, 8),
+                                                   (1024, 8, 256, 128, 2), (40, 8, 256, 128, 2)])
+def test_persistent_grouped_launches_match(tuning_env, t, e, hidden, inter, top_k):
+    """PLM_MOE_PERSIST=1 (a measurement option) runs the grouped GEMMs as persistent launches:
+    each workgroup walks several items and loads the next one's first K step during the
+    current one's epilogue. The arithmetic per item is unchanged, so the block (fused SwiGLU
+    gate_up, down with the 16-byte epilogue) and a plain grouped GEMM on every small tile
+    shape must give the same bits as the default launches."""
+    g = 128
+    h, experts, weights, gu, dn = _moe_case(t, e, hidden, inter, top_k, g, seed=t + 3)
+    args = (to_dev(h, torch.bfloat16), to_dev(experts.astype(np.int32)), to_dev(weights), gu[:2], dn[:2], inter, g)
+    counts = SMALL_COUNTS[32] + [130, 300]
+    w, s, _ = _experts(len(counts), 200, 1536, g, seed=12)
+    x = to_dev(O.bf16_round(np.random.default_rng(4).standard_normal((sum(counts), 1536)).astype(np.float32)),
+               torch.bfloat16)
+    off = to_dev(np.cumsum(counts).astype(np.int32))
+    results = []
+    for knob in (None, "1"):
+        tuning_env("PLM_MOE_PERSIST", knob)
+        out, _ = ops.routed_experts_int4_cuda(*args)
+        results.append((out, ops.grouped_gemm_int4_cuda(x, w, s, off, 200, g)))
+    assert torch.equal(results[0][0], results[1][0]), "persistent MoE block"
+    assert torch.equal(results[0][1], results[1][1]), "persistent grouped GEMM"
