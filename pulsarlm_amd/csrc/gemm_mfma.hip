@@ -326,7 +326,7 @@ __global__ void __launch_bounds__(WM * WN * 64) mfma_kernel(mfma_args a) {
         // K step read (the other one holds the next item's first loads).
         if (VO && a.splits == 1 && (a.n & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
             constexpr int EROW = 32 * NS + 16;
-            static_assert(1024 + NW * 16 * EROW <= (PERSIST ? STAGE : 2 * STAGE), "epilogue staging fits");
+            static_assert(!VO || 1024 + NW * 16 * EROW <= (PERSIST ? STAGE : 2 * STAGE), "epilogue staging fits");
             __syncthreads();  // every wavefront is past the K loop's last reads of the stages
             // Past the split-K arrival flag.
             uint8_t* ew = lds + (PERSIST ? last_stage * STAGE : 0) + 1024 + wave * 16 * EROW;
