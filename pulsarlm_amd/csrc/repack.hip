@@ -304,9 +304,12 @@ int check_common(const char* op, plm_dtype scale_dtype, int64_t n, int64_t k, in
 
 // The scale-domain flag of the int4 repacks: one word per device in static device memory,
 // addressed through hipGetSymbolAddress, cleared by a fill kernel before each checked repack
-// and read back (with a stream synchronization: repacks run at load time) after it.
+// and read back (with a stream synchronization: repacks run at load time) after it. Checked
+// repacks hold g_check_mutex from the clear to the read, so that repacks from several host
+// threads do not share one flag.
 __device__ uint32_t scale_domain_flag;
 std::mutex g_flag_mutex;
+std::mutex g_check_mutex;
 void* g_flag[64];
 
 __global__ void clear_flag_kernel(uint32_t* p) { *p = 0u; }
@@ -354,7 +357,9 @@ int launch_scale_repack(const char* op, const void* src, plm_dtype dt, int64_t n
     // fp16 scales are below 65520 in magnitude: only fp32 and bf16 int4 scales are checked.
     const int check = !int4 ? 0 : dt == PLM_FP32 ? 1 : dt == PLM_BF16 ? 2 : 0;
     uint32_t* flag = nullptr;
+    std::unique_lock<std::mutex> exclusive(g_check_mutex, std::defer_lock);
     if (check != 0) {
+        exclusive.lock();
         if (int rc = scale_flag_of_current_device(op, &flag)) return rc;
         clear_flag_kernel<<<1, 1, 0, stream>>>(flag);
         PLM_HIP_LAUNCH_CHECK(op);
@@ -470,7 +475,9 @@ int plm_convert_marlin(plm_format format, const int32_t* weight_marlin, const fl
     if (stotal > 0) {
         const int check = format == PLM_INT4 ? 1 : 0;
         uint32_t* flag = nullptr;
+        std::unique_lock<std::mutex> exclusive(g_check_mutex, std::defer_lock);
         if (check != 0) {
+            exclusive.lock();
             if (int rc = scale_flag_of_current_device(op, &flag)) return rc;
             clear_flag_kernel<<<1, 1, 0, s>>>(flag);
             PLM_HIP_LAUNCH_CHECK(op);

@@ -486,6 +486,45 @@ def test_int4_scales_beyond_the_domain_are_rejected(sdt):
             ops.repack_int4_marlin_cuda(to_dev(packed), st, 1, g)
 
 
+def test_int4_scale_check_from_several_threads():
+    """The repack's scale check uses one flag per device. Repacks from two host threads, each
+    on its own stream, one thread with an out-of-domain scale and one with valid scales, must
+    each get their own verdict: the valid weights repack to the same bits as alone, and every
+    out-of-domain repack is refused."""
+    import threading
+
+    n, k, g = 64, 512, 128
+    packed, _ = int4_case(n, k, g, 1, seed=9)
+    good = np.full((n, k // g), 0.03, np.float32)
+    bad = good.copy()
+    bad[7, 2] = 2.0**121
+    pk = to_dev(packed)
+    ref_w, ref_s = ops.repack_int4_marlin_cuda(pk, to_dev(good), 1, g)
+    torch.cuda.synchronize()
+    results = {"good": [], "bad": []}
+
+    def worker(kind, scales):
+        stream = torch.cuda.Stream()
+        st = to_dev(scales)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            for _ in range(20):
+                try:
+                    w, sc = ops.repack_int4_marlin_cuda(pk, st, 1, g)
+                    stream.synchronize()
+                    results[kind].append(torch.equal(w, ref_w) and torch.equal(sc, ref_s))
+                except Exception as e:  # noqa: BLE001 - the refusal is the expected outcome for "bad"
+                    results[kind].append("below 2^120" in str(e) and "refused")
+
+    threads = [threading.Thread(target=worker, args=("good", good)), threading.Thread(target=worker, args=("bad", bad))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert results["good"] == [True] * 20, results["good"]
+    assert results["bad"] == ["refused"] * 20, results["bad"]
+
+
 @pytest.mark.parametrize("m,k,n", [(1, 4096, 6144), (4, 4096, 24576), (1, 12288, 512), (3, 12288, 512)])
 def test_int4_scales_across_ranges_exact(m, k, n):
     """Scales mostly ordinary, with scattered groups below 2^-17 or at 2^16 and above, and one
