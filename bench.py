@@ -294,12 +294,18 @@ def section_prefill(b: Bench):
             rec = {"us": round(tt * 1e6, 1), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 3),
                    "plan": {key: v for key, v in plan.items() if key != "skip_reduction_build"}}
             if plan["k_splits"] > 1 or plan["tail_tiles"]:
+                saved = os.environ.get("PLM_MFMA_UNSPLIT")
                 os.environ["PLM_MFMA_UNSPLIT"] = "1"
                 L.reload_tuning()
-                tu = b.time(launches, reps=2 if m == 4096 else 4) / len(copies)
-                up = mfma_plan(b, m, n, k)
-                del os.environ["PLM_MFMA_UNSPLIT"]
-                L.reload_tuning()
+                try:
+                    tu = b.time(launches, reps=2 if m == 4096 else 4) / len(copies)
+                    up = mfma_plan(b, m, n, k)
+                finally:
+                    if saved is None:
+                        del os.environ["PLM_MFMA_UNSPLIT"]
+                    else:
+                        os.environ["PLM_MFMA_UNSPLIT"] = saved
+                    L.reload_tuning()
                 rec["no_split_us"] = round(tu * 1e6, 1)
                 rec["no_split_plan"] = f"{up['tile']} x{up['tiles']}"
             out[f"{name}_m{m}"] = rec
