@@ -306,3 +306,24 @@ def test_persistent_grouped_launches_match(tuning_env, t, e, hidden, inter, top_
         results.append((out, ops.grouped_gemm_int4_cuda(x, w, s, off, 200, g)))
     assert torch.equal(results[0][0], results[1][0]), "persistent MoE block"
     assert torch.equal(results[0][1], results[1][1]), "persistent grouped GEMM"
+
+
+@pytest.mark.parametrize("tile_rows", ["16", "32", "64"])
+@pytest.mark.parametrize("sdt,xdt,g", [("fp32", "bf16", 128), ("bf16", "fp16", 128), ("fp16", "fp16", 256),
+                                       ("fp16", "bf16", 64)])
+def test_persistent_grouped_small_tiles_match(tuning_env, sdt, xdt, g, tile_rows):
+    """The persistent grouped launches on each single-level tile shape (PLM_MOE_ROWS), with
+    every scale dtype, fp16 and bf16 x and groups of 64 / 128 / 256 rows of K, against the
+    default launches bit for bit."""
+    counts = [70, 0, 3, 1, 0, 0, 20, 2, 33, 0, 0, 64, 5, 9]
+    e, n, k = len(counts), 200, 1536
+    w, s, _ = _experts(e, n, k, g, seed=31, scale_dtype=sdt, x_dtype=xdt)
+    x = to_dev(O.round_to(np.random.default_rng(8).standard_normal((sum(counts), k)).astype(np.float32), xdt),
+               TDT[xdt])
+    off = to_dev(np.cumsum(counts).astype(np.int32))
+    tuning_env("PLM_MOE_ROWS", tile_rows)
+    out = []
+    for knob in (None, "1"):
+        tuning_env("PLM_MOE_PERSIST", knob)
+        out.append(ops.grouped_gemm_int4_cuda(x, w, s, off, n, g))
+    assert torch.equal(out[0], out[1]), f"persistent {tile_rows}-row tiles {sdt} {xdt} g={g}"
